@@ -1,0 +1,168 @@
+"""Throughput of the MI355X token sampler on its headline workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload peaked] [--cpu-budget 10]
+
+A step is one vsmp_pick_batch call over one batch of device-resident logits: the full sampler
+pipeline (penalty, top-k, softmax numerators, min-p, top-p, counter-RNG draw) for every row.
+Default workload ("peaked"): B=256 x V=151936 fp32, see verbo_amd/workloads.py. The logits are
+replicated into enough buffers (> 600 MB) that consecutive steps never find their input in the
+256 MB Infinity Cache. Prints one JSON line (stdout); progress goes to stderr.
+
+Fields: value = rows/s over the timed steps; roofline.achieved = algorithmic bytes per call /
+mean call duration (HIP events on the launch stream); cpu_baseline = the reference sampler
+compiled from its sources (oracle/_ref), or the oracle restatement when that is not built, timed
+on this host for a bounded sample of the same rows.
+"""
+import argparse
+import json
+import math
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK_GBS = 8000.0
+METRIC = "sampled rows/s + % HBM peak, full sampler, B=256 x V=151936 fp32 logits"
+DESCR = {
+    "single": "single: 1 x 49152 fp32 N(0,2.5^2)+8 spikes, H=64, repeat 1.1, temp .7, top-k 40, top-p .9",
+    "greedy": "greedy: 64 x 151936 fp32 N(0,3^2), H=256, repeat 1.15, temp 0, 10% rows with an exact max tie",
+    "peaked": ("peaked: 256 x 151936 fp32, 2*Gumbel + 12*rank^-1.1 on 2000 ids, H=512 (half boosted, "
+               "repeat_last=0), repeat 1.1, temp .8, top-k 50, top-p .95, min-p .05, per-row seeds 0..255, "
+               "counter-RNG draws"),
+    "wide": "wide: 512 x 151936 fp32 N(0,0.5^2), top-k 0, top-p .99, temp 1, no penalty",
+    "mixed": ("mixed: 1024 x 128256 fp32 N(0,2^2)+spikes, per-row temp/top-k/top-p/min-p/repeat, H U[0,2048], "
+              "25% greedy"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, budget):
+    """Time the reference sampler's pick() on this host (1 thread) for `budget` seconds over the
+    workload's rows. Uses oracle/_ref when built, else the oracle restatement."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import numpy as np
+
+    import oracle as O
+
+    params = w.params.copy()
+    params["repeat_last"] = 0
+    kind = "reference" if O.ref_available() else "port"
+    if kind == "reference":
+        secs, picks = O.ref_time_rows(w.logits, params, w.hist, w.hist_off, threads=1, budget_s=budget)
+    else:
+        lib = O.load_oracle()
+        u = np.full(w.B, 0.5)
+        picks, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget:
+            O.pick_rows(w.logits, params, w.hist, w.hist_off, u, threads=1)
+            picks += w.B
+        secs = time.perf_counter() - t0
+        del lib
+    return {"value": picks / secs, "unit": "rows/s", "cores": 1, "kind": kind,
+            "sample": f"{picks} pick() calls cycling over the {w.B} rows of the same workload for {secs:.1f} s, "
+                      f"1 thread, pick only (history accepted beforehand)"}
+
+
+def traffic_from_profiles(name):
+    """HBM bytes per call measured by rocprofv3 PMC runs (profiles/<workload>_traffic.json)."""
+    p = ROOT / "profiles" / f"{name}_traffic.json"
+    if not p.is_file():
+        return None
+    try:
+        return float(json.loads(p.read_text())["bytes_per_call"])
+    except (ValueError, KeyError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="peaked", choices=sorted(DESCR))
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0: skip)")
+    ap.add_argument("--min-buffer-mb", type=float, default=640.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the sampler has no multi-GPU path in this build (asked for "
+              f"--gpus {args.gpus}). Rows are independent; sharding is described in DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import verbo_amd as V
+    from verbo_amd import workloads as W
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    w = W.make(args.workload)
+    log(f"[bench] workload {args.workload} {w.B}x{w.V} generated in {time.perf_counter() - t0:.1f}s")
+    nbytes = w.logits.nbytes
+    nbuf = max(1, math.ceil(args.min_buffer_mb * 1e6 / nbytes))
+    host = torch.from_numpy(w.logits)
+    bufs = [host.to(dev) for _ in range(nbuf)]
+    params = V.to_device_params(w.params, dev) if w.per_row else \
+        V.Params(*[w.params[0][f].item() for f in V.SAMPLING_DTYPE.names])
+    hist = torch.from_numpy(w.hist if w.hist.size else np.zeros(1, np.int32)).to(dev)
+    hoff = torch.from_numpy(w.hist_off).to(dev)
+    out = torch.empty(w.B, dtype=torch.int32, device=dev)
+    ctx = V.Context(0)
+    stream = torch.cuda.current_stream(dev)
+
+    def step(i):
+        ctx.pick_batch(bufs[i % nbuf], params, hist, hoff, V.U_COUNTER, counter=i, out=out, stream=stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done, {nbuf} buffers x {nbytes / 1e6:.1f} MB")
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    ev[0].record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
+    total_ms = ev[0].elapsed_time(ev[-1])
+    ms_per_step = total_ms / args.steps
+    log(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (median {sorted(per)[len(per) // 2] * 1e3:.1f} "
+        f"us, wall {wall:.3f}s)")
+    alg = w.algorithmic_bytes()
+    achieved = alg / (ms_per_step * 1e-3) / 1e9
+    traffic = traffic_from_profiles(args.workload)
+    res = {
+        "metric": METRIC if args.workload == "peaked" else f"sampled rows/s, {DESCR[args.workload]}",
+        "value": w.B / (ms_per_step * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": DESCR[args.workload], "B": w.B, "V": w.V, "buffers": nbuf,
+                   "algorithmic_bytes_per_step": alg, "epilogue_dtype": "f64"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
+    }
+    if args.cpu_budget > 0:
+        log(f"[bench] cpu baseline ({args.cpu_budget:.0f}s budget)")
+        res["cpu_baseline"] = cpu_baseline(w, args.cpu_budget)
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,133 @@
+/*
+ * vsmp — verbo's token sampler on AMD Instinct MI355X (gfx950): the C ABI.
+ *
+ * The sampler semantics are those of verbo::Sampler::pick (reference src/sampler.cpp:50-109):
+ * repetition penalty over a history window, greedy argmax with lowest-index ties, top-k by
+ * (value desc, index asc), fp64 temperature-softmax numerators, min-p, top-p and an
+ * inverse-CDF draw over the sorted candidates.
+ *
+ * Conventions (those of the reference C ABI, src/capi.cpp:17-30): every entry point that can
+ * fail returns 0 (or a value >= 0) on success and -1 on error; the error text is per-thread and
+ * read with vsmp_last_error(). Device pointers are plain HIP device addresses; `stream` is a
+ * hipStream_t (NULL = the default stream). Batched calls are stream-ordered and do not
+ * synchronise the host.
+ */
+#ifndef VSMP_H
+#define VSMP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VSMP_API __attribute__((visibility("default")))
+
+/* Per-row sampling parameters: the same field order, types and size (32 bytes) as
+ * verbo::Sampling (reference include/verbo/verbo.hpp:56-64), so an array of verbo::Sampling
+ * can be passed as is. `seed` seeds the row's draw stream (see vsmp_u_mode). */
+typedef struct {
+  float temp;
+  int top_k;
+  float top_p;
+  float min_p;
+  float repeat;
+  int repeat_last;
+  unsigned long long seed;
+} vsmp_params;
+
+/* Where each non-greedy row's uniform draw u in [0,1) comes from. A greedy row (temp <= 0)
+ * draws nothing in every mode, as the reference does (src/sampler.cpp:66-70). */
+typedef enum {
+  VSMP_U_SUPPLIED = 0, /* u[r] given by the caller (device array of B doubles) */
+  VSMP_U_COUNTER = 1,  /* output `counter` of a SplitMix64 stream seeded with params.seed */
+  VSMP_U_XORSHIFT = 2  /* the reference stream (src/sampler.cpp:33-41): rng_state[2r..2r+1] is
+                          advanced in place, exactly as verbo::Sampler::unit would */
+} vsmp_u_mode;
+
+/* Row diagnostics (optional output, device array of B entries). */
+typedef struct {
+  int id;        /* picked token id (also written to out[r]) */
+  int path;      /* 0 greedy, 1 small-k (k <= 256), 2 general (radix select) */
+  int k;         /* size of the top-k prefix */
+  int keep_minp; /* candidates left after min-p */
+  int keep;      /* candidates left after top-p: the draw set */
+  int rank;      /* sorted position of the picked id (0 for greedy) */
+  int last_id;   /* id of the last candidate of the draw set */
+  int flags;     /* VSMP_FLAG_* */
+  float mx;      /* largest penalised logit */
+  int n_pen;     /* distinct in-range history ids penalised (small-k and greedy paths) */
+  double sum;    /* sum of the fp64 numerators over the top-k prefix */
+  double tot;    /* sum over the draw set */
+  double u;      /* the uniform draw used (0 for greedy) */
+  double draw_margin; /* distance of u*tot from the nearest CDF boundary, relative to tot */
+} vsmp_row_info;
+
+#define VSMP_FLAG_TOPP_NEAR 1u /* the top-p cut was within rounding distance of top_p */
+#define VSMP_FLAG_MINP_NEAR 2u /* a min-p comparison was within rounding distance */
+#define VSMP_FLAG_DRAW_NEAR 4u /* the draw was within 1e-6 (relative) of a CDF boundary */
+#define VSMP_FLAG_FALLBACK 8u  /* a slice needed the exact radix fallback (many near-max ties) */
+
+typedef struct vsmp_ctx vsmp_ctx;
+
+/* Last error of the calling thread ("" if none). Mirrors verbo_last_error (src/capi.cpp:46). */
+VSMP_API const char* vsmp_last_error(void);
+/* Library version string. Mirrors verbo_version (src/capi.cpp:48). */
+VSMP_API const char* vsmp_version(void);
+
+/* A sampling context on HIP device `device`: it owns the scratch memory of the batched path and
+ * the staging buffers of the host-pointer path. Not thread-safe: use one per host thread (the
+ * reference's Sampler is per-thread too, src/sampler.cpp:116). Returns NULL on error. */
+VSMP_API vsmp_ctx* vsmp_ctx_new(int device);
+VSMP_API void vsmp_ctx_free(vsmp_ctx* ctx);
+
+/* Batched pick over B rows of device-resident fp32 logits (row r at logits + r*ld; logits must be
+ * 16-byte aligned and ld a multiple of 4, ld >= V). Replaces B independent calls of
+ * verbo::Sampler::pick (reference src/sampler.cpp:50-109); there is no batched entry point in
+ * the reference (its server serialises requests, cli/serve.cpp:168).
+ *   params/params_per_row: params_per_row = 0 -> `params` is a HOST pointer to one struct used by
+ *       every row; 1 -> a DEVICE array of B structs.
+ *   hist/hist_off: device CSR of per-row histories, oldest first (row r = hist[hist_off[r] ..
+ *       hist_off[r+1]), hist_off has B+1 entries); both NULL for no history. The window
+ *       (repeat_last) and de-duplication rules are the reference's (src/sampler.cpp:53-65).
+ *   u_mode/u/rng_state/counter: see vsmp_u_mode (unused pointers may be NULL).
+ *   out: device int[B] picked ids. info: optional device vsmp_row_info[B].
+ *   cand_ids/cand_pr/cand_cap: optional device arrays [B][cand_cap]: the first min(keep,
+ *       cand_cap) draw-set ids in sorted order and their fp64 numerators (small-k path only;
+ *       rows on the other paths leave them untouched).
+ * Calls that share a context must be issued from one host thread; calls on different streams
+ * with one context must not overlap. Returns 0, or -1 (bad arguments, HIP error). */
+VSMP_API int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
+                             const vsmp_params* params, int params_per_row, const int* hist,
+                             const int* hist_off, int u_mode, const double* u,
+                             unsigned long long* rng_state, unsigned long long counter, int* out,
+                             vsmp_row_info* info, int* cand_ids, double* cand_pr, int cand_cap,
+                             void* stream);
+
+/* One pick on a HOST logits row with a host history and a supplied draw u: the computation of
+ * verbo::Sampler::pick(logits, n) (reference src/sampler.cpp:50-109) for a sampler whose history
+ * is hist[0..H) and whose next stream draw is u. Copies the row to the device, runs the kernels
+ * on the context's stream and waits. Writes the id to *out_id (and *info if not NULL).
+ * Returns 0, or -1 (n <= 0, bad arguments, HIP error). */
+VSMP_API int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params* params,
+                            const int* hist, int H, double u, int* out_id, vsmp_row_info* info);
+
+/* A drop-in sampler object: verbo::Sampler (reference include/verbo/verbo.hpp:116-132) behind
+ * a C handle, for FFI callers. Its history, xorshift stream and seeding are the reference's
+ * (src/sampler.cpp:24-48); pick runs on the GPU through the calling thread's context. */
+typedef struct vsmp_sampler vsmp_sampler;
+/* Sampler::Sampler(Sampling), src/sampler.cpp:24. NULL on error. */
+VSMP_API vsmp_sampler* vsmp_sampler_new(const vsmp_params* cfg);
+VSMP_API void vsmp_sampler_free(vsmp_sampler* s);
+/* Sampler::pick(logits, n) on a host row, src/sampler.cpp:50-109. Returns the id or -1. */
+VSMP_API int vsmp_sampler_pick(vsmp_sampler* s, const float* logits, int n);
+/* Sampler::accept, src/sampler.cpp:43-48. */
+VSMP_API void vsmp_sampler_accept(vsmp_sampler* s, int tok);
+/* Sampler::reset, src/sampler.cpp:26-31. */
+VSMP_API void vsmp_sampler_reset(vsmp_sampler* s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,124 @@
+"""Shared test helpers: run the HIP sampler through the C ABI and the oracle on the same inputs,
+then compare with the reference's tolerance rules.
+
+Comparison rules (the north-star parity bar):
+- greedy ids, penalised sets, top-k/min-p/top-p candidate sets: bit-exact, except where the
+  oracle's own decision margin is below rounding distance (|acc - top_p| < 1e-11,
+  |pr - thr| / thr < 1e-13), which are counted;
+- probabilities (fp64 numerators, sums): within 1e-5 relative;
+- sampled ids: equal unless the draw lies within 1e-6 (relative) of a CDF boundary, counted.
+"""
+import sys
+
+import numpy as np
+
+import oracle as O
+import verbo_amd as V
+
+NEAR_TOPP = 1e-11
+NEAR_MINP = 1e-13
+NEAR_DRAW = 1e-6
+PROB_RTOL = 1e-5
+
+
+def log(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def csr(hists):
+    off = np.zeros(len(hists) + 1, np.int32)
+    off[1:] = np.cumsum([len(h) for h in hists])
+    flat = np.concatenate([np.asarray(h, np.int32) for h in hists]) if off[-1] else np.zeros(0, np.int32)
+    return flat.astype(np.int32), off
+
+
+class Run:
+    """One batched GPU pick and the oracle's answer on the same inputs."""
+
+    def __init__(self, ctx, logits, params, hist=None, hist_off=None, u=None, cand_cap=0, ld=None, device="cuda"):
+        import torch
+
+        self.logits = np.ascontiguousarray(logits, np.float32)
+        B, Vv = self.logits.shape
+        self.B, self.V = B, Vv
+        self.params = np.ascontiguousarray(params, dtype=V.SAMPLING_DTYPE)
+        per_row = self.params.size == B and B > 1
+        if u is None:
+            u = np.array([O.counter_u(int(self.params[r if per_row else 0]["seed"]), r) for r in range(B)])
+        self.u = np.asarray(u, np.float64)
+        ld = ld or ((Vv + 3) // 4 * 4)
+        buf = torch.zeros((B, ld), dtype=torch.float32)
+        buf[:, :Vv] = torch.from_numpy(self.logits)
+        dl = buf.to(device)[:, :Vv]
+        dh = dho = None
+        if hist is not None:
+            dh = torch.from_numpy(np.ascontiguousarray(hist, np.int32) if len(hist) else np.zeros(1, np.int32)).to(device)
+            dho = torch.from_numpy(np.ascontiguousarray(hist_off, np.int32)).to(device)
+        du = torch.from_numpy(self.u).to(device)
+        info = torch.zeros(B * 72, dtype=torch.uint8, device=device)
+        cid = cpr = None
+        if cand_cap:
+            cid = torch.full((B, cand_cap), -1, dtype=torch.int32, device=device)
+            cpr = torch.zeros((B, cand_cap), dtype=torch.float64, device=device)
+        pr = V.Params(*[self.params[0][f].item() for f in V.SAMPLING_DTYPE.names]) if not per_row else \
+            V.to_device_params(self.params, device)
+        out = ctx.pick_batch(_rows_view(dl), pr, dh, dho, V.U_SUPPLIED, du, info=info, cand_ids=cid, cand_pr=cpr)
+        torch.cuda.synchronize()
+        self.ids = out.cpu().numpy()
+        self.info = V.row_info(info)
+        self.cand = cid.cpu().numpy() if cid is not None else None
+        self.cand_pr = cpr.cpu().numpy() if cpr is not None else None
+        self.cand_cap = cand_cap
+        self.o_ids, self.o_info, self.o_cand, self.o_pr = O.pick_rows(self.logits, self.params, hist, hist_off,
+                                                                      self.u, cand_cap=cand_cap)
+
+    def report(self):
+        """Checks every row; returns (n_near_draw, n_mismatch_near) and raises on real mismatches."""
+        gi, oi = self.info, self.o_info
+        problems = []
+        near = 0
+        near_mismatch = 0
+        for r in range(self.B):
+            o = oi[r]
+            g = gi[r]
+            set_amb = o["topp_margin"] < NEAR_TOPP or o["minp_margin"] < NEAR_MINP
+            draw_amb = o["draw_margin"] < NEAR_DRAW
+            near += int(draw_amb)
+            if g["id"] != self.ids[r]:
+                problems.append(f"row {r}: out {self.ids[r]} != info.id {g['id']}")
+            if o["greedy"]:
+                if self.ids[r] != self.o_ids[r]:
+                    problems.append(f"row {r}: greedy id {self.ids[r]} != oracle {self.o_ids[r]}")
+                continue
+            if g["k"] != o["k"]:
+                problems.append(f"row {r}: k {g['k']} != {o['k']}")
+            if not set_amb and (g["keep_minp"] != o["keep_minp"] or g["keep"] != o["keep"]):
+                problems.append(f"row {r}: keep ({g['keep_minp']},{g['keep']}) != ({o['keep_minp']},{o['keep']})")
+            if not np.float32(g["mx"]) == np.float32(o["mx"]):
+                problems.append(f"row {r}: mx {g['mx']} != {o['mx']}")
+            if abs(g["sum"] - o["sum"]) > PROB_RTOL * abs(o["sum"]):
+                problems.append(f"row {r}: sum {g['sum']} vs {o['sum']}")
+            if not set_amb and abs(g["tot"] - o["tot"]) > PROB_RTOL * abs(o["tot"]):
+                problems.append(f"row {r}: tot {g['tot']} vs {o['tot']}")
+            if self.ids[r] != self.o_ids[r]:
+                if draw_amb or set_amb:
+                    near_mismatch += 1
+                else:
+                    problems.append(f"row {r}: id {self.ids[r]} != oracle {self.o_ids[r]} "
+                                    f"(draw margin {o['draw_margin']:.3g}, keep {o['keep']})")
+            if self.cand is not None and g["path"] == V.PATH_SMALLK and not set_amb:
+                m = min(int(o["keep"]), self.cand_cap)
+                if not (self.cand[r, :m] == self.o_cand[r, :m]).all():
+                    problems.append(f"row {r}: candidate ids differ")
+                p, q = self.cand_pr[r, :m], self.o_pr[r, :m]
+                if (np.abs(p - q) > PROB_RTOL * np.abs(q)).any():
+                    problems.append(f"row {r}: candidate probabilities differ by {np.max(np.abs(p - q) / q):.3g}")
+        if problems:
+            raise AssertionError(f"{len(problems)} problems:\n" + "\n".join(problems[:20]))
+        return near, near_mismatch
+
+
+def _rows_view(t):
+    """A [B, V] view whose row stride may exceed V (the padded device buffer)."""
+    return t

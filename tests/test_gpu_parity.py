@@ -1,0 +1,212 @@
+"""Parity of the HIP sampler with the reference, through the C ABI, on an MI355X.
+
+Mirrors the reference's sampler tests (tests/test_core.cpp:454-496) and extends them: golden
+picks recorded from the compiled reference, every stage against the oracle on seeded random
+batches, all five workloads (reduced and full size), the three draw modes and the edge cases.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import verbo_amd as V
+from helpers import Run, csr, log
+from verbo_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+KAT = np.array([0.1, 3.0, 2.9, -1.0, 0.0], np.float32)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import torch
+
+    assert torch.cuda.is_available(), "the gpu tests need a ROCm device"
+    return V.Context(0)
+
+
+def test_reference_kats_on_gpu():
+    """tests/test_core.cpp:454-496 through the drop-in verbo::Sampler."""
+    log("kats")
+    assert V.Sampler(temp=0.0).pick(KAT) == 1
+    a, b = V.Sampler(seed=42, top_k=2, top_p=1.0), V.Sampler(seed=42, top_k=2, top_p=1.0)
+    c1 = 0
+    for _ in range(400):
+        x = a.pick(KAT)
+        assert x == b.pick(KAT)
+        assert x in (1, 2)
+        c1 += x == 1
+    assert 150 < c1 < 300
+    sp = V.Sampler(seed=1, top_k=0, top_p=0.5)
+    assert all(sp.pick(KAT) == 1 for _ in range(100))
+    sm = V.Sampler(seed=1, top_k=0, top_p=1.0, min_p=0.5)
+    assert all(sm.pick(KAT) in (1, 2) for _ in range(100))
+    sr = V.Sampler(temp=0.0, repeat=2.0)
+    sr.accept(1)
+    assert sr.pick(KAT) == 2
+    sr.reset()
+    assert sr.pick(KAT) == 1
+    with pytest.raises(V.VsmpError):
+        V.Sampler().pick(np.zeros(0, np.float32))
+
+
+def test_golden_reference_sequences(golden):
+    """The drop-in Sampler on the GPU replays every pick the compiled reference recorded:
+    same seeds, histories, accepts -> the same ids."""
+    bad = []
+    for c in golden:
+        log("golden", c["name"], c["logits"].size)
+        s = V.Sampler(V.Params(*[getattr(c["cfg"], f) for f, _ in O.Sampling._fields_]))
+        for t in c["hist"]:
+            s.accept(int(t))
+        got = []
+        for _ in range(c["n"]):
+            got.append(s.pick(c["logits"]))
+            if c["accept"]:
+                s.accept(got[-1])
+        if got != c["ids"].tolist():
+            bad.append((c["name"], got[:8], c["ids"][:8].tolist()))
+    assert not bad, bad
+
+
+def _random_batch(rng, B, Vv, per_row=True, ties=False):
+    scale = rng.choice([0.05, 1.0, 3.0, 10.0])
+    lg = rng.normal(0, scale, (B, Vv)).astype(np.float32)
+    if ties:
+        lg = np.round(lg).astype(np.float32)
+    n = B if per_row else 1
+    p = np.zeros(n, V.SAMPLING_DTYPE)
+    p["temp"] = rng.choice([0.0, 0.3, 0.7, 1.0, 1.6], n)
+    p["top_k"] = rng.choice([0, 1, 2, 40, 256, 257, 1000, Vv - 1, Vv + 3], n)
+    p["top_p"] = rng.choice([0.0, 0.5, 0.9, 0.99, 1.0], n)
+    p["min_p"] = rng.choice([0.0, 0.0, 0.05, 0.3, 1.5], n)
+    p["repeat"] = rng.choice([1.0, 1.2, 0.8], n)
+    p["repeat_last"] = rng.choice([0, 3, 64, -1], n)
+    p["seed"] = rng.integers(1, 1 << 62, n)
+    hists = [rng.integers(-2, Vv + 2, int(rng.integers(0, 300))) for _ in range(B)]
+    h, off = csr(hists)
+    return lg, p, h, off
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_batches_match_oracle(ctx, seed):
+    rng = np.random.default_rng(100 + seed)
+    for Vv in (1, 3, 5, 64, 257, 1023, 4099, 20000):
+        B = int(rng.integers(1, 40))
+        lg, p, h, off = _random_batch(rng, B, Vv, per_row=bool(seed % 2 == 0), ties=seed % 3 == 0)
+        log("random", seed, B, Vv)
+        run = Run(ctx, lg, p, h, off, cand_cap=256)
+        run.report()
+
+
+def test_edge_rows(ctx):
+    Vv = 777
+    rows = []
+    r = np.zeros(Vv, np.float32)
+    rows.append(r)                                  # all equal
+    r = np.full(Vv, -np.inf, np.float32)
+    r[5] = 1.0
+    rows.append(r)                                  # one finite value
+    r = np.zeros(Vv, np.float32)
+    r[::2] = -0.0
+    r[100] = r[200] = 3.0
+    rows.append(r)                                  # signed zeros, exact tie at the max
+    r = np.arange(Vv, dtype=np.float32)
+    rows.append(r)                                  # ascending: the adversarial order
+    r = -np.arange(Vv, dtype=np.float32)
+    rows.append(r)                                  # descending
+    r = np.random.default_rng(0).normal(0, 1, Vv).astype(np.float32)
+    r[300:] = 2.5
+    rows.append(r)                                  # a large tie group near the top
+    lg = np.stack(rows)
+    for temp, top_k, top_p, min_p in [(0.0, 40, 0.9, 0.0), (0.7, 40, 0.9, 0.0), (1.0, 0, 1.0, 0.0),
+                                      (1.0, 0, 0.5, 0.0), (0.5, 600, 0.95, 0.1), (2.0, 3, 0.99, 2.0),
+                                      (1e-3, 0, 0.9, 0.0), (1.0, Vv, 0.0, 0.0)]:
+        p = V.params_array(n=1, temp=temp, top_k=top_k, top_p=top_p, min_p=min_p, repeat=1.3, repeat_last=0,
+                           seed=3)
+        hists = [[5, 5, 100, -1, Vv, 700]] * len(rows)
+        h, off = csr(hists)
+        log("edge", temp, top_k, top_p, min_p)
+        for u in (0.0, 0.37, 1.0 - 2.0 ** -53):
+            Run(ctx, lg, p, h, off, u=np.full(len(rows), u), cand_cap=64).report()
+
+
+def test_no_history_and_padded_rows(ctx):
+    rng = np.random.default_rng(9)
+    lg = rng.normal(0, 2, (7, 1001)).astype(np.float32)
+    p = V.params_array(n=1, temp=0.9, top_k=50, top_p=0.9, min_p=0.02, seed=5)
+    log("padded ld")
+    Run(ctx, lg, p, None, None, ld=1024, cand_cap=50).report()
+    Run(ctx, lg, p, *csr([[]] * 7), ld=1100, cand_cap=50).report()
+
+
+@pytest.mark.parametrize("name", ["single", "greedy", "peaked", "wide", "mixed"])
+def test_workloads_reduced(ctx, name):
+    w = W.make(name, rows=32)
+    log("workload", name, w.B, w.V)
+    n, nm = Run(ctx, w.logits, w.params, w.hist, w.hist_off, cand_cap=256).report()
+    log(f"  near-boundary draws {n}, mismatches among them {nm}")
+
+
+@pytest.mark.parametrize("name", ["greedy", "peaked", "wide", "mixed"])
+def test_workloads_full_size(ctx, name):
+    w = W.make(name)
+    log("workload full", name, w.B, w.V)
+    n, nm = Run(ctx, w.logits, w.params, w.hist, w.hist_off, cand_cap=128).report()
+    log(f"  near-boundary draws {n} of {w.B}, mismatches among them {nm}")
+    assert nm <= max(1, n // 10)
+
+
+def test_draw_modes(ctx):
+    import torch
+
+    rng = np.random.default_rng(4)
+    B, Vv = 48, 5000
+    lg = rng.normal(0, 2, (B, Vv)).astype(np.float32)
+    p = np.zeros(B, V.SAMPLING_DTYPE)
+    p["temp"] = np.where(np.arange(B) % 4 == 0, 0.0, 0.8)
+    p["top_k"] = np.where(np.arange(B) % 3 == 0, 0, 40)
+    p["top_p"], p["min_p"], p["repeat"], p["repeat_last"] = 0.9, 0.0, 1.0, 64
+    p["seed"] = np.arange(1, B + 1)
+    d = torch.from_numpy(lg).cuda()
+    dp = V.to_device_params(p)
+    # counter mode: u = output `counter` of the row's SplitMix64 stream
+    for counter in (0, 5):
+        log("counter mode", counter)
+        ids = ctx.pick_batch(d, dp, u_mode=V.U_COUNTER, counter=counter).cpu().numpy()
+        u = np.array([O.counter_u(int(p["seed"][r]), counter) for r in range(B)])
+        o = O.pick_rows(lg, p, u=u)[0]
+        assert (ids == o).all()
+    # xorshift mode: the reference stream of each row, advanced once per non-greedy pick
+    st = np.zeros((B, 2), np.uint64)
+    for r in range(B):
+        s = O.rng_seed(int(p["seed"][r]))
+        st[r] = [s[0], s[1]]
+    dst = torch.from_numpy(st.view(np.int64).copy()).cuda()
+    for step in range(3):
+        log("xorshift mode", step)
+        ids = ctx.pick_batch(d, dp, u_mode=V.U_XORSHIFT, rng_state=dst).cpu().numpy()
+        u = np.zeros(B)
+        for r in range(B):
+            if p["temp"][r] > 0:
+                s = (O.ctypes.c_uint64 * 2)(int(st[r, 0]), int(st[r, 1]))
+                u[r] = O.rng_unit(s)
+                st[r] = [s[0], s[1]]
+        o = O.pick_rows(lg, p, u=u)[0]
+        assert (ids == o).all()
+        assert (dst.cpu().numpy().view(np.uint64) == st).all()
+
+
+def test_bad_arguments(ctx):
+    import torch
+
+    d = torch.zeros((2, 8), device="cuda")
+    p = V.Params()
+    with pytest.raises(V.VsmpError, match="u is required"):
+        ctx.pick_batch(d, p, u_mode=V.U_SUPPLIED)
+    with pytest.raises(V.VsmpError, match="ld must be"):
+        ctx.pick_batch(torch.zeros((2, 16), device="cuda")[:, :7].contiguous().as_strided((2, 7), (7, 1)), p)
+    with pytest.raises(V.VsmpError, match="aligned"):
+        ctx.pick_batch(torch.zeros(40, device="cuda")[1:33].view(2, 16), p)
+    with pytest.raises(V.VsmpError, match="rng_state"):
+        ctx.pick_batch(d, p, u_mode=V.U_XORSHIFT)

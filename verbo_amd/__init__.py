@@ -1,0 +1,267 @@
+"""verbo's token sampler on AMD Instinct MI355X: Python bindings of libvsmp.so (include/vsmp.h).
+
+Mirrors the reference's ctypes layer (python/verbo/__init__.py): a library loader that honours
+an environment override, a parameter struct laid out like verbo::Sampling, errors raised from
+the library's per-thread message. Device buffers are torch tensors on a ROCm device; only their
+addresses cross the C ABI.
+
+    ctx = Context()
+    ids = ctx.pick_batch(logits, Params(temp=.8, top_k=50), u_mode=U_COUNTER)  # logits: cuda [B,V]
+    s = Sampler(temp=.7, seed=42); s.accept(3); tok = s.pick(numpy_row)        # verbo::Sampler
+"""
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+from .workloads import SAMPLING_DTYPE
+
+__all__ = ["Context", "Sampler", "Params", "RowInfo", "VsmpError", "load_library", "U_SUPPLIED", "U_COUNTER",
+           "U_XORSHIFT", "ROW_INFO_DTYPE", "SAMPLING_DTYPE"]
+__version__ = "0.1.0"
+
+U_SUPPLIED, U_COUNTER, U_XORSHIFT = 0, 1, 2
+FLAG_TOPP_NEAR, FLAG_MINP_NEAR, FLAG_DRAW_NEAR, FLAG_FALLBACK = 1, 2, 4, 8
+PATH_GREEDY, PATH_SMALLK, PATH_GENERAL = 0, 1, 2
+
+
+class VsmpError(RuntimeError):
+    pass
+
+
+class Params(ctypes.Structure):
+    """vsmp_params == verbo::Sampling (reference include/verbo/verbo.hpp:56-64); defaults are the
+    reference's."""
+
+    _fields_ = [
+        ("temp", ctypes.c_float),
+        ("top_k", ctypes.c_int),
+        ("top_p", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+        ("repeat", ctypes.c_float),
+        ("repeat_last", ctypes.c_int),
+        ("seed", ctypes.c_ulonglong),
+    ]
+
+    def __init__(self, temp=0.7, top_k=40, top_p=0.9, min_p=0.0, repeat=1.0, repeat_last=64, seed=0):
+        super().__init__(temp, top_k, top_p, min_p, repeat, repeat_last, seed)
+
+
+class RowInfo(ctypes.Structure):
+    _fields_ = [
+        ("id", ctypes.c_int),
+        ("path", ctypes.c_int),
+        ("k", ctypes.c_int),
+        ("keep_minp", ctypes.c_int),
+        ("keep", ctypes.c_int),
+        ("rank", ctypes.c_int),
+        ("last_id", ctypes.c_int),
+        ("flags", ctypes.c_int),
+        ("mx", ctypes.c_float),
+        ("n_pen", ctypes.c_int),
+        ("sum", ctypes.c_double),
+        ("tot", ctypes.c_double),
+        ("u", ctypes.c_double),
+        ("draw_margin", ctypes.c_double),
+    ]
+
+
+ROW_INFO_DTYPE = np.dtype([("id", "i4"), ("path", "i4"), ("k", "i4"), ("keep_minp", "i4"), ("keep", "i4"),
+                           ("rank", "i4"), ("last_id", "i4"), ("flags", "i4"), ("mx", "f4"), ("n_pen", "i4"),
+                           ("sum", "f8"), ("tot", "f8"), ("u", "f8"), ("draw_margin", "f8")])
+assert ROW_INFO_DTYPE.itemsize == ctypes.sizeof(RowInfo) == 72
+assert SAMPLING_DTYPE.itemsize == ctypes.sizeof(Params) == 32
+
+_lib = None
+_P = ctypes.c_void_p
+
+
+def _candidates():
+    env = os.environ.get("VSMP_LIB")
+    if env:
+        yield Path(env)
+    yield Path(__file__).resolve().parent / "libvsmp.so"
+
+
+def load_library():
+    """Load libvsmp.so (VSMP_LIB overrides the in-tree path). Raises VsmpError if it is missing:
+    there is no fallback implementation."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    for p in _candidates():
+        if p.is_file():
+            lib = ctypes.CDLL(str(p))
+            break
+    else:
+        raise VsmpError("libvsmp.so not found; build it with `python -m verbo_amd.build` or set VSMP_LIB")
+    sig = {
+        "vsmp_last_error": (ctypes.c_char_p, []),
+        "vsmp_version": (ctypes.c_char_p, []),
+        "vsmp_ctx_new": (_P, [ctypes.c_int]),
+        "vsmp_ctx_free": (None, [_P]),
+        "vsmp_pick_batch": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, _P, ctypes.c_int,
+                                           _P, _P, ctypes.c_int, _P, _P, ctypes.c_ulonglong, _P, _P, _P, _P,
+                                           ctypes.c_int, _P]),
+        "vsmp_pick_host": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.POINTER(Params), _P, ctypes.c_int,
+                                          ctypes.c_double, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(RowInfo)]),
+        "vsmp_sampler_new": (_P, [ctypes.POINTER(Params)]),
+        "vsmp_sampler_free": (None, [_P]),
+        "vsmp_sampler_pick": (ctypes.c_int, [_P, _P, ctypes.c_int]),
+        "vsmp_sampler_accept": (None, [_P, ctypes.c_int]),
+        "vsmp_sampler_reset": (None, [_P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _err():
+    return VsmpError(_lib.vsmp_last_error().decode("utf-8", "replace"))
+
+
+def version():
+    return load_library().vsmp_version().decode()
+
+
+def _addr(t):
+    """Device address of a torch tensor (None stays None)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise VsmpError("expected a device tensor")
+    if not t.is_contiguous():
+        raise VsmpError("expected a contiguous tensor")
+    return t.data_ptr()
+
+
+DEFAULTS = {"temp": 0.7, "top_k": 40, "top_p": 0.9, "min_p": 0.0, "repeat": 1.0, "repeat_last": 64, "seed": 0}
+
+
+def params_array(rows=None, n=None, **fields):
+    """A SAMPLING_DTYPE array: from a list of dicts/Params, or `n` copies of the given fields
+    (missing fields take the reference's defaults)."""
+    if rows is None:
+        rows = [fields] * int(n or 1)
+    out = np.zeros(len(rows), dtype=SAMPLING_DTYPE)
+    for i, r in enumerate(rows):
+        if isinstance(r, Params):
+            r = {f: getattr(r, f) for f, _ in Params._fields_}
+        d = dict(DEFAULTS, **r)
+        for f in SAMPLING_DTYPE.names:
+            out[f][i] = d[f]
+    return out
+
+
+def to_device_params(arr, device="cuda"):
+    """Upload a SAMPLING_DTYPE array as a device byte tensor for per-row parameters."""
+    import torch
+
+    a = np.ascontiguousarray(arr, dtype=SAMPLING_DTYPE)
+    return torch.from_numpy(a.view(np.uint8).copy()).to(device)
+
+
+def row_info(t):
+    """Host numpy ROW_INFO_DTYPE view of a device info tensor (uint8, B*72 bytes)."""
+    return t.cpu().numpy().view(ROW_INFO_DTYPE)
+
+
+class Context:
+    """A vsmp_ctx on one device: scratch for batched picks, staging for host picks."""
+
+    def __init__(self, device=0):
+        load_library()
+        self._h = _lib.vsmp_ctx_new(int(device))
+        if not self._h:
+            raise _err()
+        self.device = device
+
+    def close(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.vsmp_ctx_free(h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def pick_batch(self, logits, params, hist=None, hist_off=None, u_mode=U_COUNTER, u=None, rng_state=None,
+                   counter=0, out=None, info=None, cand_ids=None, cand_pr=None, stream=None):
+        """vsmp_pick_batch on torch device tensors. `params`: a Params (shared by all rows) or a
+        device byte tensor from to_device_params (one entry per row). Returns `out` (int32 [B]).
+        Stream-ordered on `stream` (default: torch's current stream); does not synchronise."""
+        import torch
+
+        if logits.dim() != 2 or logits.dtype != torch.float32:
+            raise VsmpError("logits must be a 2-D float32 device tensor")
+        B, V = logits.shape
+        ld = logits.stride(0)
+        if logits.stride(1) != 1:
+            raise VsmpError("logits rows must be contiguous")
+        if out is None:
+            out = torch.empty(B, dtype=torch.int32, device=logits.device)
+        if isinstance(params, Params):
+            pp, per_row = ctypes.addressof(params), 0
+        else:
+            if params.numel() != 32 * B:
+                raise VsmpError("per-row params must hold B entries")
+            pp, per_row = _addr(params), 1
+        cap = 0
+        if cand_ids is not None:
+            cap = cand_ids.shape[1]
+        st = stream if stream is not None else torch.cuda.current_stream(logits.device)
+        if not logits.is_cuda:
+            raise VsmpError("logits must be a device tensor")
+        rc = _lib.vsmp_pick_batch(self._h, logits.data_ptr(), B, V, ld, pp, per_row, _addr(hist), _addr(hist_off),
+                                  int(u_mode), _addr(u), _addr(rng_state), int(counter), _addr(out), _addr(info),
+                                  _addr(cand_ids), _addr(cand_pr), cap, ctypes.c_void_p(st.cuda_stream))
+        if rc != 0:
+            raise _err()
+        return out
+
+    def pick_host(self, logits, params, hist=(), u=0.0, with_info=False):
+        """vsmp_pick_host: one pick on a host row (numpy). Returns id (and RowInfo)."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        h = np.ascontiguousarray(hist, dtype=np.int32)
+        out = ctypes.c_int(-1)
+        info = RowInfo()
+        rc = _lib.vsmp_pick_host(self._h, lg.ctypes.data_as(_P), lg.size, ctypes.byref(params),
+                                 h.ctypes.data_as(_P) if h.size else None, h.size, float(u), ctypes.byref(out),
+                                 ctypes.byref(info) if with_info else None)
+        if rc != 0:
+            raise _err()
+        return (out.value, info) if with_info else out.value
+
+
+class Sampler:
+    """verbo::Sampler (reference include/verbo/verbo.hpp:116-132) with pick on the GPU."""
+
+    def __init__(self, params=None, **kw):
+        load_library()
+        p = params if params is not None else Params(**kw)
+        self._h = _lib.vsmp_sampler_new(ctypes.byref(p))
+        if not self._h:
+            raise _err()
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.vsmp_sampler_free(h)
+            self._h = None
+
+    def pick(self, logits):
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        r = _lib.vsmp_sampler_pick(self._h, lg.ctypes.data_as(_P), lg.size)
+        if r < 0:
+            raise _err()
+        return r
+
+    def accept(self, tok):
+        _lib.vsmp_sampler_accept(self._h, int(tok))
+
+    def reset(self):
+        _lib.vsmp_sampler_reset(self._h)

@@ -1,0 +1,299 @@
+// C ABI of the MI355X sampler: contexts, argument checks, scratch memory and kernel launches.
+//
+// Error convention of the reference C ABI (src/capi.cpp:17-30): failures return -1 (or NULL) and
+// leave a per-thread message for vsmp_last_error().
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "vsmp.h"
+#include "vsmp_common.hpp"
+#include "vsmp_error.hpp"
+
+namespace vsmp {
+
+namespace {
+thread_local std::string g_err;
+}
+
+int set_error(const std::string& msg) {
+  g_err = msg;
+  return -1;
+}
+void clear_error() { g_err.clear(); }
+
+namespace {
+
+bool hip_ok(hipError_t e, const char* what) {
+  if (e == hipSuccess) return true;
+  set_error(std::string("vsmp: ") + what + ": " + hipGetErrorString(e));
+  return false;
+}
+
+template <class T>
+bool grow(T*& p, size_t& cap, size_t need, bool zero, const char* what) {
+  if (need <= cap && p) return true;
+  size_t n = std::max<size_t>(need, cap * 2);
+  if (p) {
+    // a kernel launched earlier may still read the old buffer
+    if (!hip_ok(hipDeviceSynchronize(), "synchronise before growing scratch")) return false;
+    (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+  void* q = nullptr;
+  if (!hip_ok(hipMalloc(&q, n * sizeof(T)), what)) return false;
+  if (zero && !hip_ok(hipMemset(q, 0, n * sizeof(T)), what)) {
+    (void)hipFree(q);
+    return false;
+  }
+  p = static_cast<T*>(q);
+  cap = n;
+  return true;
+}
+
+int path_host(const vsmp_params& p, int V, bool smallk_ok) {
+  if (p.temp <= 0.0f) return kPathGreedy;
+  const int k = (p.top_k > 0 && p.top_k < V) ? p.top_k : V;
+  return (smallk_ok && k <= kKmax) ? kPathSmallK : kPathGeneral;
+}
+
+}  // namespace
+}  // namespace vsmp
+
+struct vsmp_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;  // used by the host-pointer path
+  // batched-path scratch
+  unsigned long long* s_cand = nullptr;
+  size_t n_cand = 0;
+  int* s_cnt = nullptr;
+  size_t n_cnt = 0;
+  int* s_npen = nullptr;
+  size_t n_npen = 0;
+  unsigned long long* s_max = nullptr;
+  size_t n_max = 0;
+  unsigned int* s_min = nullptr;
+  size_t n_min = 0;
+  unsigned int* s_bits = nullptr;
+  size_t n_bits = 0;
+  unsigned int* tickets = nullptr;
+  size_t n_tickets = 0;
+  // host-pointer path buffers
+  float* d_logits = nullptr;
+  size_t n_logits = 0;
+  int* d_hist = nullptr;
+  size_t n_hist = 0;
+  int* d_hoff = nullptr;
+  size_t n_hoff = 0;
+  double* d_u = nullptr;
+  size_t n_u = 0;
+  int* d_out = nullptr;
+  size_t n_out = 0;
+  vsmp_row_info* d_info = nullptr;
+  size_t n_info = 0;
+};
+
+namespace vsmp {
+namespace {
+
+struct Plan {
+  int ept, S, L, grid, xcd, smallk_ok;
+  bool any_general, any_smallk;
+};
+
+// Slice shape: enough workgroups to fill the chip (>= 2048), slices of 256*EPT elements, and no
+// more slices than the small-k merge can hold (S * k <= kMergeCap).
+Plan plan(int B, int V, const vsmp_params* hostp) {
+  Plan pl{};
+  int kk = kKmax;  // largest small-k k a row may ask for
+  bool uniform_path = false;
+  int upath = 0;
+  if (hostp) {
+    uniform_path = true;
+    const int k = (hostp->top_k > 0 && hostp->top_k < V) ? hostp->top_k : V;
+    kk = std::min(k, kKmax);
+    upath = path_host(*hostp, V, true);
+  }
+  const bool need_merge = !uniform_path || upath == kPathSmallK;
+  const int epts[3] = {64, 32, 16};
+  pl.ept = 64;
+  for (int e : epts) {
+    const int L = kTpb * e;
+    const int S = (V + L - 1) / L;
+    if (need_merge && (static_cast<long long>(S) * kk > kMergeCap || S > kMaxMergeSlices)) break;
+    pl.ept = e;
+    if (static_cast<long long>(B) * S >= 2048) break;
+  }
+  pl.L = kTpb * pl.ept;
+  pl.S = (V + pl.L - 1) / pl.L;
+  pl.smallk_ok = (static_cast<long long>(pl.S) * kk <= kMergeCap && pl.S <= kMaxMergeSlices) ? 1 : 0;
+  pl.xcd = B >= 8 ? 1 : 0;
+  pl.grid = pl.xcd ? 8 * ((B + 7) / 8) * pl.S : B * pl.S;
+  if (uniform_path) {
+    const int p = path_host(*hostp, V, pl.smallk_ok != 0);
+    pl.any_general = p == kPathGeneral;
+    pl.any_smallk = p == kPathSmallK;
+  } else {
+    pl.any_general = true;
+    pl.any_smallk = pl.smallk_ok != 0;
+  }
+  return pl;
+}
+
+int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
+               int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
+               unsigned long long* rng_state, unsigned long long counter, int* out, vsmp_row_info* info,
+               int* cand_ids, double* cand_pr, int cand_cap, hipStream_t st) {
+  if (!ctx) return set_error("vsmp: null context");
+  if (!logits || !out || !params) return set_error("vsmp: logits, params and out are required");
+  if (B < 1 || V < 1) return set_error("vsmp: need B >= 1 and V >= 1");
+  if (V > kMaxVocab) return set_error("vsmp: vocabulary larger than " + std::to_string(kMaxVocab));
+  if (ld < V || (ld & 3) != 0) return set_error("vsmp: ld must be >= V and a multiple of 4");
+  if ((reinterpret_cast<uintptr_t>(logits) & 15u) != 0) return set_error("vsmp: logits must be 16-byte aligned");
+  if ((hist == nullptr) != (hist_off == nullptr)) return set_error("vsmp: hist and hist_off go together");
+  if (u_mode == VSMP_U_SUPPLIED && !u) return set_error("vsmp: u is required with VSMP_U_SUPPLIED");
+  if (u_mode == VSMP_U_XORSHIFT && !rng_state) return set_error("vsmp: rng_state is required with VSMP_U_XORSHIFT");
+  if (u_mode < VSMP_U_SUPPLIED || u_mode > VSMP_U_XORSHIFT) return set_error("vsmp: unknown u_mode");
+  if (cand_cap < 0 || (cand_cap > 0 && !cand_ids)) return set_error("vsmp: cand_ids is required with cand_cap > 0");
+  const Plan pl = plan(B, V, params_per_row ? nullptr : params);
+  const size_t slots = static_cast<size_t>(B) * static_cast<size_t>(pl.S);
+  if (slots > static_cast<size_t>(INT32_MAX) / kKmax) return set_error("vsmp: batch too large");
+  const int words = (V + 31) / 32;
+  if (!grow(ctx->s_cnt, ctx->n_cnt, slots, false, "scratch") || !grow(ctx->s_npen, ctx->n_npen, slots, false, "scratch") ||
+      !grow(ctx->s_max, ctx->n_max, slots, false, "scratch") || !grow(ctx->s_min, ctx->n_min, slots, false, "scratch") ||
+      !grow(ctx->tickets, ctx->n_tickets, static_cast<size_t>(B), true, "scratch"))
+    return -1;
+  if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch")) return -1;
+  if (pl.any_general && hist && !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch"))
+    return -1;
+
+  KArgs a{};
+  a.logits = logits;
+  a.ld = ld;
+  a.B = B;
+  a.V = V;
+  if (params_per_row) {
+    a.params = params;
+  } else {
+    a.params = nullptr;
+    a.shared = *params;
+  }
+  a.hist = hist;
+  a.hist_off = hist_off;
+  a.u_mode = u_mode;
+  a.u = u;
+  a.rng = rng_state;
+  a.counter = counter;
+  a.out = out;
+  a.info = info;
+  a.cand_ids = cand_ids;
+  a.cand_pr = cand_pr;
+  a.cand_cap = cand_cap;
+  a.S = pl.S;
+  a.L = pl.L;
+  a.xcd_map = pl.xcd;
+  a.smallk_ok = pl.smallk_ok;
+  a.s_cand = ctx->s_cand;
+  a.s_cnt = ctx->s_cnt;
+  a.s_npen = ctx->s_npen;
+  a.s_max = ctx->s_max;
+  a.s_min = ctx->s_min;
+  a.s_bits = ctx->s_bits;
+  a.words = words;
+  a.tickets = ctx->tickets;
+  launch_stage1(a, pl.ept, pl.grid, st);
+  if (!hip_ok(hipGetLastError(), "stage-1 launch")) return -1;
+  if (pl.any_general) {
+    launch_general(a, st);
+    if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace vsmp
+
+extern "C" {
+
+const char* vsmp_last_error(void) { return vsmp::g_err.c_str(); }
+
+const char* vsmp_version(void) { return "0.1.0"; }
+
+vsmp_ctx* vsmp_ctx_new(int device) {
+  vsmp::clear_error();
+  int dev = device;
+  if (dev < 0 && !vsmp::hip_ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+  if (!vsmp::hip_ok(hipSetDevice(dev), "hipSetDevice")) return nullptr;
+  vsmp_ctx* c = new vsmp_ctx();
+  c->device = dev;
+  if (!vsmp::hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate")) {
+    delete c;
+    return nullptr;
+  }
+  return c;
+}
+
+void vsmp_ctx_free(vsmp_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipDeviceSynchronize();
+  void* bufs[] = {c->s_cand, c->s_cnt, c->s_npen, c->s_max, c->s_min, c->s_bits, c->tickets,
+                  c->d_logits, c->d_hist, c->d_hoff, c->d_u, c->d_out, c->d_info};
+  for (void* p : bufs)
+    if (p) (void)hipFree(p);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
+                    int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
+                    unsigned long long* rng_state, unsigned long long counter, int* out, vsmp_row_info* info,
+                    int* cand_ids, double* cand_pr, int cand_cap, void* stream) {
+  vsmp::clear_error();
+  if (ctx && !vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  return vsmp::pick_batch(ctx, logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
+                          out, info, cand_ids, cand_pr, cand_cap, static_cast<hipStream_t>(stream));
+}
+
+int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params* params, const int* hist, int H,
+                   double u, int* out_id, vsmp_row_info* info) {
+  using vsmp::grow;
+  using vsmp::hip_ok;
+  vsmp::clear_error();
+  if (!ctx || !logits || !params || !out_id) return vsmp::set_error("vsmp: null argument");
+  if (n <= 0) return vsmp::set_error("vsmp: pick needs at least one logit");
+  if (H < 0 || (H > 0 && !hist)) return vsmp::set_error("vsmp: bad history");
+  if (!hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  const long long ld = (n + 3) & ~3;
+  if (!grow(ctx->d_logits, ctx->n_logits, static_cast<size_t>(ld), false, "host-path buffers") ||
+      !grow(ctx->d_hist, ctx->n_hist, static_cast<size_t>(std::max(H, 1)), false, "host-path buffers") ||
+      !grow(ctx->d_hoff, ctx->n_hoff, 2, false, "host-path buffers") ||
+      !grow(ctx->d_u, ctx->n_u, 1, false, "host-path buffers") ||
+      !grow(ctx->d_out, ctx->n_out, 1, false, "host-path buffers") ||
+      !grow(ctx->d_info, ctx->n_info, 1, false, "host-path buffers"))
+    return -1;
+  hipStream_t st = ctx->stream;
+  const int hoff[2] = {0, H};
+  if (!hip_ok(hipMemcpyAsync(ctx->d_logits, logits, sizeof(float) * static_cast<size_t>(n), hipMemcpyHostToDevice, st),
+              "copy logits") ||
+      (H > 0 && !hip_ok(hipMemcpyAsync(ctx->d_hist, hist, sizeof(int) * static_cast<size_t>(H), hipMemcpyHostToDevice, st),
+                        "copy history")) ||
+      !hip_ok(hipMemcpyAsync(ctx->d_hoff, hoff, sizeof hoff, hipMemcpyHostToDevice, st), "copy history offsets") ||
+      !hip_ok(hipMemcpyAsync(ctx->d_u, &u, sizeof u, hipMemcpyHostToDevice, st), "copy u"))
+    return -1;
+  if (vsmp::pick_batch(ctx, ctx->d_logits, 1, n, ld, params, 0, H > 0 ? ctx->d_hist : nullptr,
+                       H > 0 ? ctx->d_hoff : nullptr, VSMP_U_SUPPLIED, ctx->d_u, nullptr, 0, ctx->d_out,
+                       info ? ctx->d_info : nullptr, nullptr, nullptr, 0, st) != 0)
+    return -1;
+  if (!hip_ok(hipMemcpyAsync(out_id, ctx->d_out, sizeof(int), hipMemcpyDeviceToHost, st), "copy id") ||
+      (info && !hip_ok(hipMemcpyAsync(info, ctx->d_info, sizeof(vsmp_row_info), hipMemcpyDeviceToHost, st), "copy info")) ||
+      !hip_ok(hipStreamSynchronize(st), "synchronise"))
+    return -1;
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,62 @@
+// Shared between the HIP kernels and the host launch code: constants, kernel arguments.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "vsmp.h"
+
+namespace vsmp {
+
+constexpr int kTpb = 256;        // threads per slice workgroup
+constexpr int kKmax = 256;       // largest top-k served by the small-k path (== kTpb, see stage 1)
+constexpr int kCandCap = 2048;   // per-slice LDS candidate capacity before the radix fallback
+constexpr int kMergeCap = 4096;  // per-row LDS capacity of the last-slice merge
+constexpr int kMaxMergeSlices = 64;  // slices a small-k row may be cut into
+constexpr int kGenThreads = 1024;  // threads per general-path workgroup (one row each)
+constexpr int kGenBuckets = 4096;  // level-0 mass buckets of the general path
+constexpr int kGenCap = 2048;      // elements the general path sorts in LDS at once
+constexpr int kMaxVocab = 1 << 26;
+
+enum RowPath : int { kPathGreedy = 0, kPathSmallK = 1, kPathGeneral = 2 };
+
+// Arguments of both kernels (passed by value).
+struct KArgs {
+  const float* logits;
+  long long ld;
+  int B;
+  int V;
+  const vsmp_params* params;  // device array (per_row) or null
+  vsmp_params shared;         // the parameters of every row when params is null
+  const int* hist;
+  const int* hist_off;
+  int u_mode;
+  const double* u;
+  unsigned long long* rng;
+  unsigned long long counter;
+  int* out;
+  vsmp_row_info* info;
+  int* cand_ids;
+  double* cand_pr;
+  int cand_cap;
+  // slicing: row r is cut into S slices of L = kTpb * EPT elements
+  int S;
+  int L;
+  int xcd_map;     // 1: the S slices of a row are dispatched to one XCD
+  int smallk_ok;   // 0: rows with k <= kKmax still take the general path (merge would overflow)
+  // scratch (device, owned by the context)
+  unsigned long long* s_cand;  // [B*S][kKmax] sorted slice top-k (composite keys)
+  int* s_cnt;                  // [B*S] entries in s_cand (bit 30: the slice used the fallback)
+  int* s_npen;                 // [B*S] penalised ids in the slice
+  unsigned long long* s_max;   // [B*S] slice maximum (composite key)
+  unsigned int* s_min;         // [B*S] slice minimum (order key)
+  unsigned int* s_bits;        // [B][words] penalty bitmaps of general-path rows
+  int words;                   // bitmap words per row
+  unsigned int* tickets;       // [B] slice arrival counters (self-resetting)
+};
+
+void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st);
+void launch_general(const KArgs& a, hipStream_t st);
+
+}  // namespace vsmp
