@@ -40,7 +40,8 @@ typedef struct {
  * draws nothing in every mode, as the reference does (src/sampler.cpp:66-70). */
 typedef enum {
   VSMP_U_SUPPLIED = 0, /* u[r] given by the caller (device array of B doubles) */
-  VSMP_U_COUNTER = 1,  /* output `counter` of a SplitMix64 stream seeded with params.seed */
+  VSMP_U_COUNTER = 1,  /* output `counter` of a SplitMix64 stream seeded with the row's
+                          params.seed (per-row parameters) or with seed + r (shared parameters) */
   VSMP_U_XORSHIFT = 2  /* the reference stream (src/sampler.cpp:33-41): rng_state[2r..2r+1] is
                           advanced in place, exactly as verbo::Sampler::unit would */
 } vsmp_u_mode;

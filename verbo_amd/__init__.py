@@ -90,6 +90,13 @@ def load_library():
     global _lib
     if _lib is not None:
         return _lib
+    # torch ships its own HIP runtime under the same soname (libamdhip64.so.7). Whichever loads
+    # first serves the whole process, and torch cannot use a newer one; so when torch is present
+    # it is loaded first and this library, its kernels and torch's streams share its runtime.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     for p in _candidates():
         if p.is_file():
             lib = ctypes.CDLL(str(p))

@@ -80,8 +80,6 @@ struct vsmp_ctx {
   size_t n_min = 0;
   unsigned int* s_bits = nullptr;
   size_t n_bits = 0;
-  unsigned int* tickets = nullptr;
-  size_t n_tickets = 0;
   // host-pointer path buffers
   float* d_logits = nullptr;
   size_t n_logits = 0;
@@ -102,7 +100,7 @@ namespace {
 
 struct Plan {
   int ept, S, L, grid, xcd, smallk_ok;
-  bool any_general, any_smallk;
+  bool any_general, any_smallk, any_finish;
 };
 
 // Slice shape: enough workgroups to fill the chip (>= 2048), slices of 256*EPT elements, and no
@@ -137,9 +135,11 @@ Plan plan(int B, int V, const vsmp_params* hostp) {
     const int p = path_host(*hostp, V, pl.smallk_ok != 0);
     pl.any_general = p == kPathGeneral;
     pl.any_smallk = p == kPathSmallK;
+    pl.any_finish = p != kPathGeneral;
   } else {
     pl.any_general = true;
     pl.any_smallk = pl.smallk_ok != 0;
+    pl.any_finish = true;
   }
   return pl;
 }
@@ -164,8 +164,7 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   if (slots > static_cast<size_t>(INT32_MAX) / kKmax) return set_error("vsmp: batch too large");
   const int words = (V + 31) / 32;
   if (!grow(ctx->s_cnt, ctx->n_cnt, slots, false, "scratch") || !grow(ctx->s_npen, ctx->n_npen, slots, false, "scratch") ||
-      !grow(ctx->s_max, ctx->n_max, slots, false, "scratch") || !grow(ctx->s_min, ctx->n_min, slots, false, "scratch") ||
-      !grow(ctx->tickets, ctx->n_tickets, static_cast<size_t>(B), true, "scratch"))
+      !grow(ctx->s_max, ctx->n_max, slots, false, "scratch") || !grow(ctx->s_min, ctx->n_min, slots, false, "scratch"))
     return -1;
   if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch")) return -1;
   if (pl.any_general && hist && !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch"))
@@ -204,9 +203,12 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   a.s_min = ctx->s_min;
   a.s_bits = ctx->s_bits;
   a.words = words;
-  a.tickets = ctx->tickets;
   launch_stage1(a, pl.ept, pl.grid, st);
   if (!hip_ok(hipGetLastError(), "stage-1 launch")) return -1;
+  if (pl.any_finish) {
+    launch_finish(a, st);
+    if (!hip_ok(hipGetLastError(), "finish launch")) return -1;
+  }
   if (pl.any_general) {
     launch_general(a, st);
     if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
@@ -241,7 +243,7 @@ void vsmp_ctx_free(vsmp_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
-  void* bufs[] = {c->s_cand, c->s_cnt, c->s_npen, c->s_max, c->s_min, c->s_bits, c->tickets,
+  void* bufs[] = {c->s_cand, c->s_cnt, c->s_npen, c->s_max, c->s_min, c->s_bits,
                   c->d_logits, c->d_hist, c->d_hoff, c->d_u, c->d_out, c->d_info};
   for (void* p : bufs)
     if (p) (void)hipFree(p);

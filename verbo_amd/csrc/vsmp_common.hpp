@@ -53,10 +53,10 @@ struct KArgs {
   unsigned int* s_min;         // [B*S] slice minimum (order key)
   unsigned int* s_bits;        // [B][words] penalty bitmaps of general-path rows
   int words;                   // bitmap words per row
-  unsigned int* tickets;       // [B] slice arrival counters (self-resetting)
 };
 
 void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st);
+void launch_finish(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
 
 }  // namespace vsmp

@@ -5,13 +5,14 @@
 // ~index. Larger composite = earlier in the reference's sort order (value desc, index asc,
 // src/sampler.cpp:71), so every selection below is exact and independent of summation order.
 //
-// Two kernels:
-//  k_stage1  grid = rows x slices. Each workgroup loads one slice of one row into registers (a
+// Three kernels, stream-ordered (each kernel boundary publishes the previous one's results; no
+// workgroup waits on another):
+//  k_stage1  grid = rows x slices. Each workgroup loads one slice of one row into registers (the
 //            single HBM pass), applies the repetition penalty from an LDS bitmap of the row's
-//            history window, and computes its slice maximum. Small-k rows (k <= 256) also select
-//            the slice's exact top-k; greedy and small-k rows are finished by the last slice to
-//            arrive (atomic ticket), which merges the slices and runs the reference's sequential
-//            fp64 epilogue (softmax numerators, min-p, top-p, inverse-CDF draw).
+//            history window, and writes its slice maximum; small-k rows (k <= 256) also write the
+//            slice's exact, sorted top-k.
+//  k_finish  one workgroup per greedy / small-k row: merges the slice results and runs the
+//            reference's sequential fp64 epilogue (softmax numerators, min-p, top-p, draw).
 //  k_general one workgroup per remaining row (k > 256 or top-k off): multi-pass radix select by
 //            count and by fp64 mass over the row, with histograms in LDS.
 #include <cfloat>
@@ -75,7 +76,10 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {  // SplitMix64 output fu
 __device__ double draw_u(const KArgs& a, int row, const vsmp_params& p) {
   if (a.u_mode == VSMP_U_SUPPLIED) return a.u[row];
   if (a.u_mode == VSMP_U_COUNTER) {
-    const uint64_t z = mix64(p.seed + (a.counter + 1ull) * kGamma);
+    // row r's stream is seeded with its own params.seed, or with seed + r when all rows share one
+    // parameter block
+    const uint64_t seed = a.params ? p.seed : p.seed + static_cast<uint64_t>(row);
+    const uint64_t z = mix64(seed + (a.counter + 1ull) * kGamma);
     return static_cast<double>(z >> 11) * kTwoM53;
   }
   // xorshift128+, src/sampler.cpp:33-41
@@ -331,13 +335,11 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
   constexpr int WORDS = EPT * kTpb / 32;
   __shared__ uint32_t sm_bits[WORDS];
   __shared__ __align__(16) uint32_t sm_tmax[kTpb];
-  __shared__ uint64_t sm_buf[kMergeCap];
+  __shared__ uint64_t sm_buf[kCandCap];
   __shared__ uint64_t sm_top[kKmax];
-  __shared__ double sm_pr[kKmax];
   __shared__ uint64_t sm_red64[kTpb / 64];
   __shared__ uint32_t sm_red32[kTpb / 64];
   __shared__ int sm_int[8];
-  __shared__ int sm_off[kMaxMergeSlices + 1];
 
   int row, slice;
   if (!map_block(blockIdx.x, a, row, slice)) return;
@@ -554,14 +556,26 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
     }
   }
 
-  // -- the last slice of a greedy / small-k row to arrive finishes the row
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) sm_int[4] = static_cast<int>(atomicAdd(&a.tickets[row], 1u));
-  __syncthreads();
-  if (sm_int[4] != S - 1) return;
-  __threadfence();
-  if (tid == 0) a.tickets[row] = 0u;
+}
+
+// ---- finish: one workgroup per greedy / small-k row, after stage 1 -----------------------------
+// The kernel boundary orders stage 1's slice results before these reads.
+
+__global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
+  __shared__ uint64_t sm_buf[kMergeCap];
+  __shared__ uint64_t sm_top[kKmax];
+  __shared__ double sm_pr[kKmax];
+  __shared__ uint64_t sm_red64[kTpb / 64];
+  __shared__ uint32_t sm_red32[kTpb / 64];
+  __shared__ int sm_int[8];
+  __shared__ int sm_off[kMaxMergeSlices + 1];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const vsmp_params P = row_params(a, row);
+  const int V = a.V;
+  const int S = a.S;
+  const int path = path_of(P, V, a.smallk_ok);
+  if (path == kPathGeneral) return;  // k_general finishes these rows
 
   if (path == kPathGreedy) {
     uint64_t b = 0ull;
@@ -670,7 +684,7 @@ __device__ __forceinline__ float4 load4(const float* rp, int e, int V) {
 // Calls f(composite, value) for every element of the row, penalty applied.
 template <class F>
 __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
-  constexpr int U = 4;
+  constexpr int U = 2;
   constexpr int step = kGenThreads * 4 * U;
   for (int base = 0; base < R.V; base += step) {
     float4 v[U];
@@ -1104,6 +1118,10 @@ void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st) {
       hipLaunchKernelGGL(k_stage1<64>, dim3(grid), dim3(kTpb), 0, st, a);
       break;
   }
+}
+
+void launch_finish(const KArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_finish, dim3(a.B), dim3(kTpb), 0, st, a);
 }
 
 void launch_general(const KArgs& a, hipStream_t st) {

@@ -13,7 +13,8 @@ Workloads (B rows x V vocab, fp32 logits, row-major, ld = V). Histories are pena
           second index equal to the row's penalised maximum (an exact tie).
   peaked  256 x 151936  2*Gumbel(0,1) + 12*rank^-1.1 over a random 2,000-id permutation; H=512 with
           half the ids from the boosted set; repeat 1.1, temp .8, top-k 50, top-p .95,
-          min-p .05, seeds 0..255.
+          min-p .05, seeds 0..255 (one shared parameter block with seed 0: row r draws from
+          the stream seeded with r).
   wide    512 x 151936  N(0, 0.5^2); top-k 0, top-p .99, min-p 0, temp 1, repeat 1.
   mixed   1024 x 128256  N(0, 2^2) + 1..16 spikes of +U[4,10] per row; per-row temp U[0,1.5]
           (25% exactly 0), top-k in {0,20,40,100}, top-p U[.8,1], min-p in {0,.05,.1},
@@ -176,9 +177,8 @@ def make(name, rows=None):
             h = np.concatenate([boost[_ints(s + 1, r * 512, nb, 0, 2000)], _ints(s + 2, r * 512, 512 - nb, 0, V)])
             hl.append(h)
         hist, off = _csr(hl)
+        # one shared parameter block: with seed 0, row r's draw stream is seeded with r
         p = _params(temp=0.8, top_k=50, top_p=0.95, min_p=0.05, repeat=1.1, repeat_last=0, seed=0)
-        p = np.repeat(p, B)
-        p["seed"] = np.arange(B, dtype=np.uint64)
         return Workload(name, lg, p, hist, off)
     if name == "wide":
         for r in range(B):
