@@ -17,6 +17,14 @@ pytestmark = pytest.mark.gpu
 KAT = np.array([0.1, 3.0, 2.9, -1.0, 0.0], np.float32)
 
 
+@pytest.fixture(params=["slices", "rows"])
+def mode(request, monkeypatch):
+    """Both decompositions on the same inputs: split rows (slices + merge) and one workgroup per
+    row. The library reads VSMP_MODE on every call."""
+    monkeypatch.setenv("VSMP_MODE", request.param)
+    return request.param
+
+
 @pytest.fixture(scope="module")
 def ctx():
     import torch
@@ -89,17 +97,17 @@ def _random_batch(rng, B, Vv, per_row=True, ties=False):
 
 
 @pytest.mark.parametrize("seed", range(6))
-def test_random_batches_match_oracle(ctx, seed):
+def test_random_batches_match_oracle(ctx, mode, seed):
     rng = np.random.default_rng(100 + seed)
     for Vv in (1, 3, 5, 64, 257, 1023, 4099, 20000):
         B = int(rng.integers(1, 40))
         lg, p, h, off = _random_batch(rng, B, Vv, per_row=bool(seed % 2 == 0), ties=seed % 3 == 0)
-        log("random", seed, B, Vv)
+        log("random", mode, seed, B, Vv)
         run = Run(ctx, lg, p, h, off, cand_cap=256)
         run.report()
 
 
-def test_edge_rows(ctx):
+def test_edge_rows(ctx, mode):
     Vv = 777
     rows = []
     r = np.zeros(Vv, np.float32)
@@ -126,12 +134,12 @@ def test_edge_rows(ctx):
                            seed=3)
         hists = [[5, 5, 100, -1, Vv, 700]] * len(rows)
         h, off = csr(hists)
-        log("edge", temp, top_k, top_p, min_p)
+        log("edge", mode, temp, top_k, top_p, min_p)
         for u in (0.0, 0.37, 1.0 - 2.0 ** -53):
             Run(ctx, lg, p, h, off, u=np.full(len(rows), u), cand_cap=64).report()
 
 
-def test_no_history_and_padded_rows(ctx):
+def test_no_history_and_padded_rows(ctx, mode):
     rng = np.random.default_rng(9)
     lg = rng.normal(0, 2, (7, 1001)).astype(np.float32)
     p = V.params_array(n=1, temp=0.9, top_k=50, top_p=0.9, min_p=0.02, seed=5)
@@ -141,9 +149,9 @@ def test_no_history_and_padded_rows(ctx):
 
 
 @pytest.mark.parametrize("name", ["single", "greedy", "peaked", "wide", "mixed"])
-def test_workloads_reduced(ctx, name):
+def test_workloads_reduced(ctx, mode, name):
     w = W.make(name, rows=32)
-    log("workload", name, w.B, w.V)
+    log("workload", mode, name, w.B, w.V)
     n, nm = Run(ctx, w.logits, w.params, w.hist, w.hist_off, cand_cap=256).report()
     log(f"  near-boundary draws {n}, mismatches among them {nm}")
 
@@ -157,7 +165,7 @@ def test_workloads_full_size(ctx, name):
     assert nm <= max(1, n // 10)
 
 
-def test_draw_modes(ctx):
+def test_draw_modes(ctx, mode):
     import torch
 
     rng = np.random.default_rng(4)
@@ -210,3 +218,20 @@ def test_bad_arguments(ctx):
         ctx.pick_batch(torch.zeros(40, device="cuda")[1:33].view(2, 16), p)
     with pytest.raises(V.VsmpError, match="rng_state"):
         ctx.pick_batch(d, p, u_mode=V.U_XORSHIFT)
+
+
+def test_counter_seeds_with_shared_params(ctx, mode):
+    """Shared parameters: row r draws output `counter` of the stream seeded with seed + r."""
+    import torch
+
+    w = W.make("peaked", rows=40)
+    p = w.params[0]
+    d = torch.from_numpy(w.logits).cuda()
+    h, ho = torch.from_numpy(w.hist).cuda(), torch.from_numpy(w.hist_off).cuda()
+    for counter in (0, 3):
+        log("shared counter", mode, counter)
+        ids = ctx.pick_batch(d, V.Params(*[p[f].item() for f in V.SAMPLING_DTYPE.names]), h, ho, V.U_COUNTER,
+                             counter=counter).cpu().numpy()
+        u = np.array([O.counter_u(int(p["seed"]) + r, counter) for r in range(w.B)])
+        o = O.pick_rows(w.logits, w.params, w.hist, w.hist_off, u)[0]
+        assert (ids == o).all()

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -66,6 +67,7 @@ int path_host(const vsmp_params& p, int V, bool smallk_ok) {
 
 struct vsmp_ctx {
   int device = 0;
+  int cus = 256;                 // compute units of the device
   hipStream_t stream = nullptr;  // used by the host-pointer path
   // batched-path scratch
   unsigned long long* s_cand = nullptr;
@@ -99,14 +101,44 @@ namespace vsmp {
 namespace {
 
 struct Plan {
+  bool rows;  // row mode: one workgroup per row (k_rows), else slices (k_stage1 + k_finish)
   int ept, S, L, grid, xcd, smallk_ok;
   bool any_general, any_smallk, any_finish;
 };
 
+// VSMP_MODE=rows|slices pins the decomposition (testing and tuning); default: rows when every CU
+// gets at least one row.
+int forced_mode() {
+  const char* e = std::getenv("VSMP_MODE");
+  if (!e) return -1;
+  if (std::strcmp(e, "rows") == 0) return 1;
+  if (std::strcmp(e, "slices") == 0) return 0;
+  return -1;
+}
+
 // Slice shape: enough workgroups to fill the chip (>= 2048), slices of 256*EPT elements, and no
 // more slices than the small-k merge can hold (S * k <= kMergeCap).
-Plan plan(int B, int V, const vsmp_params* hostp) {
+Plan plan(int B, int V, const vsmp_params* hostp, int cus) {
   Plan pl{};
+  const int fm = forced_mode();
+  pl.rows = V <= kRowMaxVocab && (fm == 1 || (fm == -1 && B >= cus));
+  if (pl.rows) {
+    pl.S = 1;
+    pl.ept = 0;
+    pl.L = V;
+    pl.grid = B;
+    pl.xcd = 0;
+    pl.smallk_ok = 1;
+    if (hostp) {
+      const int p = path_host(*hostp, V, true);
+      pl.any_general = p == kPathGeneral;
+    } else {
+      pl.any_general = true;
+    }
+    pl.any_smallk = false;
+    pl.any_finish = false;
+    return pl;
+  }
   int kk = kKmax;  // largest small-k k a row may ask for
   bool uniform_path = false;
   int upath = 0;
@@ -119,7 +151,14 @@ Plan plan(int B, int V, const vsmp_params* hostp) {
   const bool need_merge = !uniform_path || upath == kPathSmallK;
   const int epts[3] = {64, 32, 16};
   pl.ept = 64;
+  // VSMP_EPT (16, 32 or 64) pins the elements per thread of stage 1, for tuning
+  static const int forced = [] {
+    const char* e = std::getenv("VSMP_EPT");
+    const int v = e ? std::atoi(e) : 0;
+    return (v == 16 || v == 32 || v == 64) ? v : 0;
+  }();
   for (int e : epts) {
+    if (forced && e != forced) continue;
     const int L = kTpb * e;
     const int S = (V + L - 1) / L;
     if (need_merge && (static_cast<long long>(S) * kk > kMergeCap || S > kMaxMergeSlices)) break;
@@ -159,7 +198,7 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   if (u_mode == VSMP_U_XORSHIFT && !rng_state) return set_error("vsmp: rng_state is required with VSMP_U_XORSHIFT");
   if (u_mode < VSMP_U_SUPPLIED || u_mode > VSMP_U_XORSHIFT) return set_error("vsmp: unknown u_mode");
   if (cand_cap < 0 || (cand_cap > 0 && !cand_ids)) return set_error("vsmp: cand_ids is required with cand_cap > 0");
-  const Plan pl = plan(B, V, params_per_row ? nullptr : params);
+  const Plan pl = plan(B, V, params_per_row ? nullptr : params, ctx->cus);
   const size_t slots = static_cast<size_t>(B) * static_cast<size_t>(pl.S);
   if (slots > static_cast<size_t>(INT32_MAX) / kKmax) return set_error("vsmp: batch too large");
   const int words = (V + 31) / 32;
@@ -203,8 +242,13 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   a.s_min = ctx->s_min;
   a.s_bits = ctx->s_bits;
   a.words = words;
-  launch_stage1(a, pl.ept, pl.grid, st);
-  if (!hip_ok(hipGetLastError(), "stage-1 launch")) return -1;
+  if (pl.rows) {
+    launch_rows(a, st);
+    if (!hip_ok(hipGetLastError(), "row launch")) return -1;
+  } else {
+    launch_stage1(a, pl.ept, pl.grid, st);
+    if (!hip_ok(hipGetLastError(), "stage-1 launch")) return -1;
+  }
   if (pl.any_finish) {
     launch_finish(a, st);
     if (!hip_ok(hipGetLastError(), "finish launch")) return -1;
@@ -232,6 +276,8 @@ vsmp_ctx* vsmp_ctx_new(int device) {
   if (!vsmp::hip_ok(hipSetDevice(dev), "hipSetDevice")) return nullptr;
   vsmp_ctx* c = new vsmp_ctx();
   c->device = dev;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) c->cus = cus;
   if (!vsmp::hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate")) {
     delete c;
     return nullptr;

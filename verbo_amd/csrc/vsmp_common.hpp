@@ -18,6 +18,8 @@ constexpr int kGenThreads = 1024;  // threads per general-path workgroup (one ro
 constexpr int kGenBuckets = 4096;  // level-0 mass buckets of the general path
 constexpr int kGenCap = 2048;      // elements the general path sorts in LDS at once
 constexpr int kMaxVocab = 1 << 26;
+constexpr int kRowMaxVocab = 1 << 19;                    // row mode keeps the row's bitmap in LDS
+constexpr size_t kRowMaxDynLds = (kRowMaxVocab / 32) * 4;
 
 enum RowPath : int { kPathGreedy = 0, kPathSmallK = 1, kPathGeneral = 2 };
 
@@ -57,6 +59,7 @@ struct KArgs {
 
 void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st);
 void launch_finish(const KArgs& a, hipStream_t st);
+void launch_rows(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
 
 }  // namespace vsmp

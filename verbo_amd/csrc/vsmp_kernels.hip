@@ -227,18 +227,6 @@ __device__ void select_top(uint64_t* buf, int cnt, int ks, uint64_t* top) {
   __syncthreads();
 }
 
-// Number of entries of the descending list a[0..n) greater than x.
-__device__ __forceinline__ int count_greater(const uint64_t* a, int n, uint64_t x) {
-  int lo = 0, hi = n;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (a[mid] > x)
-      lo = mid + 1;
-    else
-      hi = mid;
-  }
-  return lo;
-}
 
 __device__ __forceinline__ bool map_block(int b, const KArgs& a, int& row, int& slice) {
   if (!a.xcd_map) {
@@ -255,104 +243,314 @@ __device__ __forceinline__ bool map_block(int b, const KArgs& a, int& row, int& 
   return row < a.B;
 }
 
-// Reference epilogue on the sorted top-k (src/sampler.cpp:79-108), executed by one thread with
-// the reference's sequential fp64 order. pr[0..k) holds the numerators.
-__device__ void finish_small(const KArgs& a, int row, const vsmp_params& P, const uint64_t* top, const double* pr,
-                             int k, int n_pen, int flags, int* keep_out) {
+// ---- wave-level epilogue -------------------------------------------------------------------------
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b)), l));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b >> 32)), l));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+constexpr int kEpiJ = kKmax / 64;  // candidates per lane
+
+// The reference epilogue (src/sampler.cpp:79-108) run by one wave on the sorted top-k in LDS.
+// Numerators and quotients are computed one per lane; every running sum is taken in the
+// reference's sequential order by a uniform loop that reads lane values with readlane (no LDS
+// round trip per element). Called by all 64 lanes of one wave.
+__device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsmp_params& P, const uint64_t* sorted,
+                                              int k, int n_pen, int flags) {
+  const int lane = threadIdx.x & 63;
+  double pr[kEpiJ], q[kEpiJ];
+  const float mx = comp_val(sorted[0]);
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j) {
+    const int i = j * 64 + lane;
+    pr[j] = i < k ? numer(comp_val(sorted[i]), mx, P.temp) : 0.0;
+  }
+  // src/sampler.cpp:84: sum in order
   double sum = 0.0;
-  for (int i = 0; i < k; ++i) sum += pr[i];
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j) {
+    const int n = min(64, k - j * 64);
+    for (int l = 0; l < n; ++l) sum += readlane_f64(pr[j], l);
+  }
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j) q[j] = pr[j] / sum;  // the same IEEE quotient as pr[i] / sum
+  // src/sampler.cpp:86-91: keep = the first i >= 1 with pr[i] < thr (pr[0] passes when min_p <= 1)
   int keep = k;
   if (P.min_p > 0.0f) {
-    const double thr = pr[0] * static_cast<double>(P.min_p);
-    keep = 1;
-    while (keep < k && pr[keep] >= thr) ++keep;
-    double mg = fabs(pr[keep - 1] - thr) / thr;
-    if (keep < k) mg = fmin(mg, fabs(pr[keep] - thr) / thr);
+    const double thr = readlane_f64(pr[0], 0) * static_cast<double>(P.min_p);
+    keep = k;
+#pragma unroll
+    for (int j = kEpiJ - 1; j >= 0; --j) {
+      const int i = j * 64 + lane;
+      const uint64_t fail = __ballot(i >= 1 && i < k && !(pr[j] >= thr));
+      if (fail) keep = j * 64 + __ffsll(static_cast<long long>(fail)) - 1;
+    }
+    // margins of the deciding comparisons
+    const int kp = keep;
+    double mg = 1e300;
+#pragma unroll
+    for (int j = 0; j < kEpiJ; ++j) {
+      const int i = j * 64 + lane;
+      if ((i == kp - 1 || i == kp) && i < k) mg = fmin(mg, fabs(pr[j] - thr) / thr);
+    }
+    for (int o = 32; o > 0; o >>= 1) mg = fmin(mg, __shfl_xor(mg, o));
     if (mg < kNearMinP) flags |= VSMP_FLAG_MINP_NEAR;
   }
   const int keep_minp = keep;
+  // src/sampler.cpp:92-100
   if (P.top_p > 0.0f && P.top_p < 1.0f) {
     const double tp = static_cast<double>(P.top_p);
     double acc = 0.0, prev = 0.0;
     int i = 0;
-    for (; i < keep; ++i) {
-      prev = acc;
-      acc += pr[i] / sum;
-      if (acc >= tp) break;
+    bool hit = false;
+#pragma unroll
+    for (int j = 0; j < kEpiJ; ++j) {
+      if (!hit) {
+        const int n = min(64, keep - j * 64);
+        for (int l = 0; l < n; ++l) {
+          prev = acc;
+          acc += readlane_f64(q[j], l);
+          if (acc >= tp) {
+            hit = true;
+            break;
+          }
+          ++i;
+        }
+      }
     }
     double mg = fabs(acc - tp);
     if (i > 0) mg = fmin(mg, fabs(prev - tp));
     if (mg < kNearTopP) flags |= VSMP_FLAG_TOPP_NEAR;
     if (i + 1 < keep) keep = i + 1;
   }
+  // src/sampler.cpp:101-108
   double tot = 0.0;
-  for (int i = 0; i < keep; ++i) tot += pr[i];
-  const double u = draw_u(a, row, P);
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j) {
+    const int n = min(64, keep - j * 64);
+    for (int l = 0; l < n; ++l) tot += readlane_f64(pr[j], l);
+  }
+  double u = 0.0;
+  if (lane == 0) u = draw_u(a, row, P);
+  u = readlane_f64(u, 0);
   double r = u * tot, before = r;
   int pick = keep - 1;
   bool picked = false;
-  for (int i = 0; i < keep; ++i) {
-    before = r;
-    r -= pr[i];
-    if (r <= 0.0) {
-      pick = i;
-      picked = true;
-      break;
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j) {
+    if (!picked) {
+      const int n = min(64, keep - j * 64);
+      for (int l = 0; l < n; ++l) {
+        before = r;
+        r -= readlane_f64(pr[j], l);
+        if (r <= 0.0) {
+          pick = j * 64 + l;
+          picked = true;
+          break;
+        }
+      }
     }
   }
   double mg = fabs(r);
   if (picked && pick > 0) mg = fmin(mg, before);
   mg = tot > 0.0 ? mg / tot : 0.0;
   if (mg < kNearDraw) flags |= VSMP_FLAG_DRAW_NEAR;
-  const int id = comp_idx(top[pick]);
-  a.out[row] = id;
-  if (a.info) {
-    vsmp_row_info inf;
-    inf.id = id;
-    inf.path = kPathSmallK;
-    inf.k = k;
-    inf.keep_minp = keep_minp;
-    inf.keep = keep;
-    inf.rank = pick;
-    inf.last_id = comp_idx(top[keep - 1]);
-    inf.flags = flags;
-    inf.mx = comp_val(top[0]);
-    inf.n_pen = n_pen;
-    inf.sum = sum;
-    inf.tot = tot;
-    inf.u = u;
-    inf.draw_margin = mg;
-    a.info[row] = inf;
+  const int id = comp_idx(sorted[pick]);
+  if (lane == 0) {
+    a.out[row] = id;
+    if (a.info) {
+      vsmp_row_info inf;
+      inf.id = id;
+      inf.path = kPathSmallK;
+      inf.k = k;
+      inf.keep_minp = keep_minp;
+      inf.keep = keep;
+      inf.rank = pick;
+      inf.last_id = comp_idx(sorted[keep - 1]);
+      inf.flags = flags;
+      inf.mx = mx;
+      inf.n_pen = n_pen;
+      inf.sum = sum;
+      inf.tot = tot;
+      inf.u = u;
+      inf.draw_margin = mg;
+      a.info[row] = inf;
+    }
   }
-  *keep_out = keep;
+  if (a.cand_ids && a.cand_cap > 0) {
+    const int m = min(keep, a.cand_cap);
+#pragma unroll
+    for (int j = 0; j < kEpiJ; ++j) {
+      const int i = j * 64 + lane;
+      if (i < m) {
+        a.cand_ids[static_cast<size_t>(row) * a.cand_cap + i] = comp_idx(sorted[i]);
+        if (a.cand_pr) a.cand_pr[static_cast<size_t>(row) * a.cand_cap + i] = pr[j];
+      }
+    }
+  }
+}
+
+// Descending bitonic sort of one value per lane across a wave64.
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const uint32_t y = __shfl_xor(x, j);
+      const bool desc = (lane & k) == 0;
+      const bool lower = (lane & j) == 0;
+      x = (lower == desc) ? max(x, y) : min(x, y);
+    }
+  }
+  return x;
+}
+
+// Entries of the descending list a[0..n) that are >= x (upper bound).
+__device__ __forceinline__ int count_ge(const uint32_t* a, int n, uint32_t x) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] >= x)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+__device__ __forceinline__ int count_gt(const uint32_t* a, int n, uint32_t x) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] > x)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
 }
 
 // ---- stage 1 ------------------------------------------------------------------------------------
+
+constexpr int kPenCap = 1024;  // penalised elements of one slice handled out of line
+
+enum SliceMode : int { kModeSmallK = 0, kModeBest = 1, kModeBestMin = 2 };
+
+// Loads one slice with the penalty applied in place (every element checks the bitmap and
+// divides where it must). Used when the out-of-line penalty list overflowed, and before the
+// exact radix fallback (which needs every key in registers).
+__device__ __forceinline__ uint32_t& lane_of(uint4& v, int c) {
+  return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
+}
+
+// Key of element e of the slice, penalty applied in place (src/sampler.cpp:53-65).
+__device__ __forceinline__ uint32_t slice_key(const float* rp, int e, bool pen, float rep, const uint32_t* bits, int lo) {
+  float f = rp[e];
+  if (pen && ((bits[(e - lo) >> 5] >> ((e - lo) & 31)) & 1u)) f = penalise(f, rep);
+  return ord_key(f);
+}
+
+// Rare exact path of a slice, streamed from global memory in runtime loops (nothing held in
+// registers): the slice maximum / minimum, or its sorted top-ks by radix select. Used when a
+// slice has more penalised elements than the side list holds, or when too many elements tie
+// near the top for the threshold pass.
+__device__ void slice_exact(const float* rp, int lo, int hi, bool pen, float rep, const uint32_t* bits, int mode,
+                            int ks, uint64_t* top, uint32_t* hist, int* ints, uint64_t* red64, uint32_t* red32,
+                            uint64_t* out_max, uint32_t* out_min) {
+  const int tid = threadIdx.x;
+  if (mode != kModeSmallK) {
+    uint64_t b = 0ull;
+    uint32_t mn = 0xFFFFFFFFu;
+    for (int e = lo + tid; e < hi; e += kTpb) {
+      const uint32_t k = slice_key(rp, e, pen, rep, bits, lo);
+      b = max64(b, comp(k, static_cast<uint32_t>(e)));
+      mn = min(mn, k);
+    }
+    *out_max = block_max64<kTpb>(b, red64);
+    *out_min = static_cast<uint32_t>(block_min64<kTpb>(mn, red64));
+    return;
+  }
+  // the ks-th largest key T, 8 bits at a time
+  uint32_t prefix = 0u, mask = 0u;
+  int need = ks;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    __syncthreads();
+    hist[tid] = 0u;
+    __syncthreads();
+    for (int e = lo + tid; e < hi; e += kTpb) {
+      const uint32_t k = slice_key(rp, e, pen, rep, bits, lo);
+      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int cum = 0, d = 255;
+      for (; d > 0; --d) {
+        if (cum + static_cast<int>(hist[d]) >= need) break;
+        cum += static_cast<int>(hist[d]);
+      }
+      ints[3] = d;
+      ints[4] = need - cum;
+    }
+    __syncthreads();
+    prefix |= static_cast<uint32_t>(ints[3]) << shift;
+    mask |= 255u << shift;
+    need = ints[4];
+  }
+  const uint32_t T = prefix;  // `need` elements equal to T are taken, lowest indices first
+  if (tid == 0) ints[1] = 0;
+  __syncthreads();
+  for (int e = lo + tid; e < hi; e += kTpb) {
+    const uint32_t k = slice_key(rp, e, pen, rep, bits, lo);
+    if (k > T) top[atomicAdd(&ints[1], 1)] = comp(k, static_cast<uint32_t>(e));
+  }
+  __syncthreads();
+  const int above = ints[1];
+  int taken = 0;
+  for (int base = lo; base < hi && taken < need; base += kTpb) {  // uniform loop, index order
+    const int e = base + tid;
+    const uint32_t m = (e < hi && slice_key(rp, e, pen, rep, bits, lo) == T) ? 1u : 0u;
+    uint32_t ex;
+    double dummy;
+    block_excl_scan<kTpb>(0.0, m, dummy, ex, reinterpret_cast<double*>(red64), red32);
+    if (m && taken + static_cast<int>(ex) < need) top[above + taken + static_cast<int>(ex)] = comp(T, static_cast<uint32_t>(e));
+    taken += static_cast<int>(block_sum_u32<kTpb>(m, red32));
+  }
+  __syncthreads();
+}
 
 template <int EPT>
 __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
   constexpr int NV = EPT / 4;
   constexpr int WORDS = EPT * kTpb / 32;
   __shared__ uint32_t sm_bits[WORDS];
-  __shared__ __align__(16) uint32_t sm_tmax[kTpb];
+  __shared__ uint32_t sm_wl[kTpb];  // 4 wave-sorted lists of per-thread maxima
   __shared__ uint64_t sm_buf[kCandCap];
+  __shared__ uint64_t sm_pen[kPenCap];
   __shared__ uint64_t sm_top[kKmax];
   __shared__ uint64_t sm_red64[kTpb / 64];
   __shared__ uint32_t sm_red32[kTpb / 64];
-  __shared__ int sm_int[8];
+  __shared__ int sm_int[8];  // 0 threshold, 1 candidates, 2 penalised, 3/4 radix digits
 
   int row, slice;
   if (!map_block(blockIdx.x, a, row, slice)) return;
   const int tid = threadIdx.x;
-  const vsmp_params P = row_params(a, row);
+  const int lane = tid & 63, wv = tid >> 6;
   const int V = a.V;
-  const int path = path_of(P, V, a.smallk_ok);
-  const int S = a.S;
   const int lo = slice * a.L;
   const int hi = min(V, lo + a.L);
-  const int slot = row * S + slice;
+  const int slot = row * a.S + slice;
+  const bool full = (hi - lo) == a.L;
+  const float* rp = a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld);
 
-  // -- penalty bitmap of this slice (src/sampler.cpp:53-65): ids of the window, in range
+  // -- 1. parameters and the history window come through the scalar cache; the history ids are
+  // loaded before the slice so that waiting for them does not wait for the slice (the vector
+  // memory counter retires loads in order)
+  const vsmp_params P = row_params(a, row);
+  const int path = path_of(P, V, a.smallk_ok);
+  const int mode = path == kPathSmallK ? kModeSmallK : (path == kPathGreedy ? kModeBest : kModeBestMin);
   int h0 = 0, h1 = 0;
   if (a.hist_off) {
     h0 = a.hist_off[row];
@@ -360,202 +558,210 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
   }
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
-  uint32_t n_pen = 0;
+  const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
+  constexpr int HPT = 8;  // history ids per thread loaded up front; longer windows loop below
+  // a fixed count of loads (clamped index; validity is tested at use, after the slice loads are
+  // issued) so that the wait for them is exact and does not wait for the slice
+  int hid[HPT];
   if (pen) {
-    const int from = (P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0;
-    for (int i = tid; i < WORDS; i += kTpb) sm_bits[i] = 0u;
-    __syncthreads();
-    for (int i = h0 + from + tid; i < h1; i += kTpb) {
-      const int id = a.hist[i];
-      if (id >= lo && id < hi) {
-        const int o = id - lo;
-        atomicOr(&sm_bits[o >> 5], 1u << (o & 31));
-      }
-    }
-    __syncthreads();
-    const int nw = (hi - lo + 31) >> 5;
-    uint32_t pc = 0;
-    for (int i = tid; i < nw; i += kTpb) {
-      pc += __popc(sm_bits[i]);
-      if (path == kPathGeneral) a.s_bits[static_cast<size_t>(row) * a.words + (lo >> 5) + i] = sm_bits[i];
-    }
-    n_pen = block_sum_u32<kTpb>(pc, sm_red32);
+#pragma unroll
+    for (int q = 0; q < HPT; ++q) hid[q] = a.hist[min(hfrom + q * kTpb + tid, h1 - 1)];
   }
 
-  // -- load the slice (all loads issued before any use), penalise, build order keys
-  const float* rp = a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld);
-  const bool full = (hi - lo) == a.L;
-  float4 raw[NV];
+  // -- 2. the slice: every load issued before any use
+  // One 16-byte load per group, never past the row: a group that starts below V ends at or below
+  // ld (both multiples of 4); groups past the slice reload its last group and are masked below.
+  uint4 d[NV];  // raw fp32 bits, converted in place to order keys
+  const uint32_t* rpu = reinterpret_cast<const uint32_t*>(rp);
+  const int elast = (hi - 1) & ~3;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int e = lo + (j * kTpb + tid) * 4;
-    if (full || e + 4 <= hi) {
-      raw[j] = *reinterpret_cast<const float4*>(rp + e);
-    } else {
-      raw[j].x = e < hi ? rp[e] : 0.0f;
-      raw[j].y = e + 1 < hi ? rp[e + 1] : 0.0f;
-      raw[j].z = e + 2 < hi ? rp[e + 2] : 0.0f;
-      raw[j].w = e + 3 < hi ? rp[e + 3] : 0.0f;
-    }
+    d[j] = *reinterpret_cast<const uint4*>(rpu + (full || e < hi ? e : elast));
   }
-  uint32_t key[EPT];
-  uint64_t best = 0ull;
-  uint32_t tmin = 0xFFFFFFFFu;
+
+  // -- 3. penalty bitmap of the slice (src/sampler.cpp:53-65)
+  if (tid == 0) {
+    sm_int[1] = 0;
+    sm_int[2] = 0;
+  }
+  if (pen) {
+    for (int i = tid; i < WORDS; i += kTpb) sm_bits[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < HPT; ++q) {
+      const int id = hid[q];
+      if (hfrom + q * kTpb + tid < h1 && id >= lo && id < hi) atomicOr(&sm_bits[(id - lo) >> 5], 1u << ((id - lo) & 31));
+    }
+    for (int i = hfrom + HPT * kTpb + tid; i < h1; i += kTpb) {
+      const int id = a.hist[i];
+      if (id >= lo && id < hi) atomicOr(&sm_bits[(id - lo) >> 5], 1u << ((id - lo) & 31));
+    }
+    __syncthreads();
+    if (path == kPathGeneral) {
+      const int nw = (hi - lo + 31) >> 5;
+      for (int i = tid; i < nw; i += kTpb) a.s_bits[static_cast<size_t>(row) * a.words + (lo >> 5) + i] = sm_bits[i];
+    }
+  } else {
+    __syncthreads();
+  }
+
+  // -- 3. order keys; penalised elements get key 0 here and are set aside in sm_pen
+  uint32_t tmax = 0u, tmin = 0xFFFFFFFFu;
+  uint32_t bk = 0u;
+  int bi = 0;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int e = lo + (j * kTpb + tid) * 4;
     uint32_t nib = 0u;
-    if (pen && e < hi) {
-      const int o = e - lo;
-      nib = (sm_bits[o >> 5] >> (o & 31)) & 0xFu;
+    if (pen && e < hi) nib = (sm_bits[(e - lo) >> 5] >> ((e - lo) & 31)) & 0xFu;
+    if (nib) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (nib & (1u << c)) {
+          const int p = atomicAdd(&sm_int[2], 1);
+          if (p < kPenCap) sm_pen[p] = (static_cast<uint64_t>(lane_of(d[j], c)) << 32) | static_cast<uint32_t>(e + c);
+        }
+      }
     }
-    const float x[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      float f = x[c];
-      if (nib & (1u << c)) f = penalise(f, P.repeat);
       const bool valid = full || e + c < hi;
-      const uint32_t k = valid ? ord_key(f) : 0u;
-      key[j * 4 + c] = k;
-      const uint64_t ck = comp(k, static_cast<uint32_t>(e + c));
-      if (valid && ck > best) best = ck;
-      if (valid && k < tmin) tmin = k;
+      uint32_t k = valid ? ord_key(__uint_as_float(lane_of(d[j], c))) : 0u;
+      k = (nib & (1u << c)) ? 0u : k;
+      lane_of(d[j], c) = k;
+      tmax = max(tmax, k);
     }
   }
+  if (mode != kModeSmallK) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int e = lo + (j * kTpb + tid) * 4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t k = lane_of(d[j], c);
+        if (k > bk) {  // increasing index order: the first maximum wins ties
+          bk = k;
+          bi = e + c;
+        }
+        if (k != 0u) tmin = min(tmin, k);
+      }
+    }
+  }
+  __syncthreads();
+  const int npen = sm_int[2];
+  const int n_pen = npen;  // distinct in-range ids of the window in this slice
+  if (npen > kPenCap) {
+    // more penalised elements than the side list holds: the exact streaming path
+    uint64_t smax = 0ull;
+    uint32_t smin = 0u;
+    const int ks = min(top_k_of(P, V), hi - lo);
+    slice_exact(rp, lo, hi, pen, P.repeat, sm_bits, mode, ks, sm_top, reinterpret_cast<uint32_t*>(sm_buf), sm_int,
+                sm_red64, sm_red32, &smax, &smin);
+    if (mode != kModeSmallK) {
+      if (tid == 0) {
+        a.s_max[slot] = smax;
+        a.s_min[slot] = smin;
+        a.s_npen[slot] = n_pen;
+      }
+      return;
+    }
+    for (int i = tid; i < ks; i += kTpb) sm_buf[i] = sm_top[i];
+    __syncthreads();
+    select_top<kTpb>(sm_buf, ks, ks, sm_top);
+    for (int i = tid; i < ks; i += kTpb) a.s_cand[static_cast<size_t>(slot) * kKmax + i] = sm_top[i];
+    if (tid == 0) {
+      a.s_cnt[slot] = ks | (1 << 30);
+      a.s_npen[slot] = n_pen;
+    }
+    return;
+  }
+  // penalised values: each divides once (src/sampler.cpp:63)
+  uint64_t pbest = 0ull;
+  uint32_t pmin = 0xFFFFFFFFu;
+  for (int j = tid; j < npen; j += kTpb) {
+    const uint64_t v = sm_pen[j];
+    const float f = penalise(__uint_as_float(static_cast<uint32_t>(v >> 32)), P.repeat);
+    const uint64_t ck = comp(ord_key(f), static_cast<uint32_t>(v));
+    sm_pen[j] = ck;
+    pbest = max64(pbest, ck);
+    pmin = min(pmin, comp_key(ck));
+  }
 
-  if (path != kPathSmallK) {
-    const uint64_t smax = block_max64<kTpb>(best, sm_red64);
-    const uint64_t smin = block_min64<kTpb>(tmin, sm_red64);
+  if (mode != kModeSmallK) {
+    const uint64_t mine = max64(bk ? comp(bk, static_cast<uint32_t>(bi)) : 0ull, pbest);
+    const uint64_t smax = block_max64<kTpb>(mine, sm_red64);
+    uint64_t smin = 0ull;
+    if (mode == kModeBestMin) smin = block_min64<kTpb>(min(tmin, pmin), sm_red64);
     if (tid == 0) {
       a.s_max[slot] = smax;
       a.s_min[slot] = static_cast<uint32_t>(smin);
-      a.s_npen[slot] = static_cast<int>(n_pen);
+      a.s_npen[slot] = n_pen;
     }
-    if (path == kPathGeneral) return;  // finished by k_general
-  } else {
-    // -- exact top-ks of the slice
-    const int k = top_k_of(P, V);
-    const int ks = min(k, hi - lo);
-    const uint32_t tk = static_cast<uint32_t>(best >> 32);  // this thread's largest key (0: none)
-    sm_tmax[tid] = tk;
-    if (tid == 0) sm_int[1] = 0;
-    __syncthreads();
-    // threshold t = the ks-th largest per-thread maximum: >= ks elements are >= t
-    int rank = 0;
-    for (int j = 0; j < kTpb; j += 4) {
-      const uint4 q = *reinterpret_cast<const uint4*>(&sm_tmax[j]);
-      rank += (q.x > tk) || (q.x == tk && j < tid);
-      rank += (q.y > tk) || (q.y == tk && j + 1 < tid);
-      rank += (q.z > tk) || (q.z == tk && j + 2 < tid);
-      rank += (q.w > tk) || (q.w == tk && j + 3 < tid);
-    }
-    if (rank == ks - 1) sm_int[0] = static_cast<int>(tk);
-    __syncthreads();
-    const uint32_t t = static_cast<uint32_t>(sm_int[0]);
-    if (tk >= t) {
-#pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        const int e = lo + (j * kTpb + tid) * 4;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t kk = key[j * 4 + c];
-          if (kk >= t && kk != 0u) {
-            const int p = atomicAdd(&sm_int[1], 1);
-            if (p < kCandCap) sm_buf[p] = comp(kk, static_cast<uint32_t>(e + c));
-          }
-        }
-      }
-    }
-    __syncthreads();
-    const int cnt = sm_int[1];
-    int flag = 0;
-    if (cnt <= kCandCap) {
-      select_top<kTpb>(sm_buf, cnt, ks, sm_top);
-    } else {
-      // Exact fallback (many elements tied near the top): radix-select the ks-th largest key T
-      // with 8-bit digits over the registers, then take every key > T and the lowest-index
-      // keys == T in index order.
-      flag = VSMP_FLAG_FALLBACK;
-      uint32_t* hist = reinterpret_cast<uint32_t*>(sm_buf);  // 256 bins
-      uint32_t prefix = 0u, mask = 0u;
-      int need = ks;
-      for (int shift = 24; shift >= 0; shift -= 8) {
-        __syncthreads();
-        hist[tid] = 0u;
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-          const uint32_t kk = key[i];
-          if (kk != 0u && (kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        if (tid == 0) {
-          int cum = 0, d = 255;
-          for (; d > 0; --d) {
-            if (cum + static_cast<int>(hist[d]) >= need) break;
-            cum += static_cast<int>(hist[d]);
-          }
-          sm_int[2] = d;
-          sm_int[3] = need - cum;
-        }
-        __syncthreads();
-        prefix |= static_cast<uint32_t>(sm_int[2]) << shift;
-        mask |= 255u << shift;
-        need = sm_int[3];
-      }
-      const uint32_t T = prefix;  // ks-th largest key; `need` copies of T are taken
-      // keys > T (fewer than ks) in any order
-      __syncthreads();
-      if (tid == 0) sm_int[1] = 0;
-      __syncthreads();
-#pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        const int e = lo + (j * kTpb + tid) * 4;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          if (key[j * 4 + c] > T) {
-            const int p = atomicAdd(&sm_int[1], 1);
-            sm_top[p] = comp(key[j * 4 + c], static_cast<uint32_t>(e + c));
-          }
-        }
-      }
-      __syncthreads();
-      const int above = sm_int[1];
-      // keys == T in increasing index order: index order is (j, tid, c)
-      int taken = 0;
-#pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        if (taken < need) {  // uniform: `taken` is a block-wide count
-          const int e = lo + (j * kTpb + tid) * 4;
-          uint32_t m = 0;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) m += key[j * 4 + c] == T;
-          uint32_t ex;
-          double dummy;
-          block_excl_scan<kTpb>(0.0, m, dummy, ex, reinterpret_cast<double*>(sm_red64), sm_red32);
-          int pos = taken + static_cast<int>(ex);
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            if (key[j * 4 + c] == T) {
-              if (pos < need) sm_top[above + pos] = comp(T, static_cast<uint32_t>(e + c));
-              ++pos;
-            }
-          }
-          taken += static_cast<int>(block_sum_u32<kTpb>(m, sm_red32));
-        }
-      }
-      __syncthreads();
-      for (int i = tid; i < ks; i += kTpb) sm_buf[i] = sm_top[i];
-      __syncthreads();
-      select_top<kTpb>(sm_buf, ks, ks, sm_top);
-    }
-    for (int i = tid; i < ks; i += kTpb) a.s_cand[static_cast<size_t>(slot) * kKmax + i] = sm_top[i];
-    if (tid == 0) {
-      a.s_cnt[slot] = ks | (flag ? (1 << 30) : 0);
-      a.s_npen[slot] = static_cast<int>(n_pen);
-    }
+    return;
   }
 
+  // -- 4. small k: the exact, sorted top-ks of the slice
+  const int k = top_k_of(P, V);
+  const int ks = min(k, hi - lo);
+  // threshold t = the ks-th largest per-thread maximum of the unpenalised elements, so at least ks
+  // elements are >= t (penalised elements can only add to them)
+  {
+    const uint32_t srt = wave_sort_desc(tmax);
+    sm_wl[wv * 64 + lane] = srt;
+    __syncthreads();
+    int rank = lane;
+#pragma unroll
+    for (int w = 0; w < kTpb / 64; ++w) {
+      if (w < wv) rank += count_ge(sm_wl + w * 64, 64, srt);
+      if (w > wv) rank += count_gt(sm_wl + w * 64, 64, srt);
+    }
+    if (rank == ks - 1) sm_int[0] = static_cast<int>(srt);
+    __syncthreads();
+  }
+  const uint32_t t = static_cast<uint32_t>(sm_int[0]);
+  if (tmax >= t) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int e = lo + (j * kTpb + tid) * 4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t kk = lane_of(d[j], c);
+        if (kk >= t && kk != 0u) {
+          const int p = atomicAdd(&sm_int[1], 1);
+          if (p < kCandCap) sm_buf[p] = comp(kk, static_cast<uint32_t>(e + c));
+        }
+      }
+    }
+  }
+  for (int j = tid; j < npen; j += kTpb) {
+    const uint64_t ck = sm_pen[j];
+    if (comp_key(ck) >= t) {
+      const int p = atomicAdd(&sm_int[1], 1);
+      if (p < kCandCap) sm_buf[p] = ck;
+    }
+  }
+  __syncthreads();
+  const int cnt = sm_int[1];
+  int flag = 0;
+  if (cnt <= kCandCap) {
+    select_top<kTpb>(sm_buf, cnt, ks, sm_top);
+  } else {
+    // Exact fallback (many elements tied near the top): stream the slice again and radix-select.
+    flag = VSMP_FLAG_FALLBACK;
+    uint64_t unused64;
+    uint32_t unused32;
+    slice_exact(rp, lo, hi, pen, P.repeat, sm_bits, kModeSmallK, ks, sm_top, reinterpret_cast<uint32_t*>(sm_buf),
+                sm_int, sm_red64, sm_red32, &unused64, &unused32);
+    for (int i = tid; i < ks; i += kTpb) sm_buf[i] = sm_top[i];
+    __syncthreads();
+    select_top<kTpb>(sm_buf, ks, ks, sm_top);
+  }
+  for (int i = tid; i < ks; i += kTpb) a.s_cand[static_cast<size_t>(slot) * kKmax + i] = sm_top[i];
+  if (tid == 0) {
+    a.s_cnt[slot] = ks | (flag ? (1 << 30) : 0);
+    a.s_npen[slot] = n_pen;
+  }
 }
 
 // ---- finish: one workgroup per greedy / small-k row, after stage 1 -----------------------------
@@ -564,7 +770,6 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
 __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
   __shared__ uint64_t sm_buf[kMergeCap];
   __shared__ uint64_t sm_top[kKmax];
-  __shared__ double sm_pr[kKmax];
   __shared__ uint64_t sm_red64[kTpb / 64];
   __shared__ uint32_t sm_red32[kTpb / 64];
   __shared__ int sm_int[8];
@@ -604,8 +809,7 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
     return;
   }
 
-  // small-k merge: every slice list is sorted; the rank of an entry in the union is its
-  // position in its own list plus the entries greater than it in the other lists
+  // small k: sort the union of the slice lists (at most kMergeCap entries), keep the first k
   const int k = top_k_of(P, V);
   if (tid == 0) {
     int off = 0, fl = 0, np = 0;
@@ -622,40 +826,37 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
   }
   __syncthreads();
   const int M = sm_off[S];
-  for (int i = tid; i < M; i += kTpb) {
-    int s = 0;
-    while (sm_off[s + 1] <= i) ++s;
-    sm_buf[i] = a.s_cand[static_cast<size_t>(row * S + s) * kKmax + (i - sm_off[s])];
-  }
-  __syncthreads();
-  for (int i = tid; i < M; i += kTpb) {
-    int s = 0;
-    while (sm_off[s + 1] <= i) ++s;
-    const uint64_t x = sm_buf[i];
-    int r = i - sm_off[s];
-    for (int s2 = 0; s2 < S && r < k; ++s2) {
-      if (s2 == s) continue;
-      r += count_greater(sm_buf + sm_off[s2], sm_off[s2 + 1] - sm_off[s2], x);
+  if (M <= 2 * kTpb) {
+    // one pass: rank of every entry among all (composites are distinct)
+    for (int i = tid; i < M; i += kTpb) {
+      int s = 0;
+      while (sm_off[s + 1] <= i) ++s;
+      sm_buf[i] = a.s_cand[static_cast<size_t>(row * S + s) * kKmax + (i - sm_off[s])];
     }
-    if (r < k) sm_top[r] = x;
-  }
-  __syncthreads();
-  const float mx = comp_val(sm_top[0]);
-  for (int i = tid; i < k; i += kTpb) sm_pr[i] = numer(comp_val(sm_top[i]), mx, P.temp);
-  __syncthreads();
-  if (tid == 0) {
-    int keep = 0;
-    finish_small(a, row, P, sm_top, sm_pr, k, sm_int[6], sm_int[5], &keep);
-    sm_int[7] = keep;
-  }
-  __syncthreads();
-  if (a.cand_ids && a.cand_cap > 0) {
-    const int m = min(sm_int[7], a.cand_cap);
-    for (int i = tid; i < m; i += kTpb) {
-      a.cand_ids[static_cast<size_t>(row) * a.cand_cap + i] = comp_idx(sm_top[i]);
-      if (a.cand_pr) a.cand_pr[static_cast<size_t>(row) * a.cand_cap + i] = sm_pr[i];
+    __syncthreads();
+    for (int i = tid; i < M; i += kTpb) {
+      const uint64_t x = sm_buf[i];
+      int r = 0;
+      for (int j = 0; j < M; ++j) r += sm_buf[j] > x;
+      if (r < k) sm_top[r] = x;
     }
+  } else {
+    int p2 = 1;
+    while (p2 < M) p2 <<= 1;
+    for (int i = tid; i < p2; i += kTpb) {
+      uint64_t v = 0ull;
+      if (i < M) {
+        int s = 0;
+        while (sm_off[s + 1] <= i) ++s;
+        v = a.s_cand[static_cast<size_t>(row * S + s) * kKmax + (i - sm_off[s])];
+      }
+      sm_buf[i] = v;
+    }
+    bitonic_desc<kTpb>(sm_buf, p2);
+    for (int i = tid; i < k; i += kTpb) sm_top[i] = sm_buf[i];
   }
+  __syncthreads();
+  if (tid < 64) epilogue_wave(a, row, P, sm_top, k, sm_int[6], sm_int[5]);
 }
 
 // ---- general path -------------------------------------------------------------------------------
@@ -1104,6 +1305,511 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   }
 }
 
+// ---- row kernel: one workgroup streams one row (batches with at least one row per CU) -------
+//
+// Sixteen waves stream the row together (wave w takes 256-element steps w, w+16, ...), four steps
+// in flight per lane. A row-level lower bound T for the k-th largest key comes from the first
+// four steps (the k-th largest of the 1024 lane maxima, rounded down to a 22-bit prefix), so
+// after the first iteration only the few elements >= T reach a wave's LDS candidate buffer. A
+// wave whose buffer fills keeps its exact top-k (wave-local sort) and then also rejects keys not
+// above its k-th key. With repeat >= 1 a penalty can only lower a value, so the stream filters on
+// unpenalised keys and only candidates are penalised (when a wave compacts, and at the end);
+// repeat < 1 penalises in the stream. At the end an exact radix select over the 64-bit
+// composites of every buffer gives the sorted top-k, then the reference epilogue runs.
+
+constexpr int kRowNT = 1024;
+constexpr int kRowW = kRowNT / 64;
+constexpr int kRowU = 4;
+constexpr int kWaveCap = 512;
+constexpr int kRowBins = 2048;
+
+struct RowShared {
+  uint64_t wbuf[kRowW][kWaveCap];
+  uint32_t bins[2][kRowBins];  // 16-byte aligned: read as uint4 by the bucket search
+  uint64_t top[kKmax];
+  uint64_t sorted[kKmax];
+  uint64_t wmax[kRowW];
+  uint64_t r64[kRowW];
+  int rank[kKmax];
+  int cnt[kRowW];
+  uint32_t npw[kRowW];
+  int ints[16];
+};
+
+// Order key without branches; +0.0f turns -0 into +0 first.
+__device__ __forceinline__ uint32_t key_of(uint32_t bits) {
+  const uint32_t b = __float_as_uint(__uint_as_float(bits) + 0.0f);
+  return b ^ (static_cast<uint32_t>(static_cast<int32_t>(b) >> 31) | 0x80000000u);
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ bool bit_of(const uint32_t* bits, int e) { return (bits[e >> 5] >> (e & 31)) & 1u; }
+
+// One wave searches 2048 bins from the top (bucket 2047 first) for the first bucket whose running
+// count reaches `need` (such a bucket is never empty). Lane l covers buckets 2047-32l down to
+// 2016-32l. out[0] = bucket (-1 when the bins hold fewer than `need`), out[1] = count above it,
+// out[2] = its own count.
+__device__ void wave_find_bucket(const uint32_t* bins, int need, int* out) {
+  const int lane = threadIdx.x & 63;
+  const int lo = kRowBins - 32 * (lane + 1);
+  const uint4* p = reinterpret_cast<const uint4*>(bins + lo);
+  uint32_t c[32];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint4 v = p[j];
+    c[4 * j] = v.x;
+    c[4 * j + 1] = v.y;
+    c[4 * j + 2] = v.z;
+    c[4 * j + 3] = v.w;
+  }
+  uint32_t s = 0;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) s += c[j];
+  uint32_t incl = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  const uint64_t m = __ballot(static_cast<int>(incl) >= need);
+  if (m == 0ull) {
+    if (lane == 0) {
+      out[0] = -1;
+      out[1] = 0;
+      out[2] = 0;
+    }
+    return;
+  }
+  if (lane == __ffsll(static_cast<long long>(m)) - 1) {
+    uint32_t run = incl - s, ab = 0, inb = 0;
+    int b = -1;
+#pragma unroll
+    for (int j = 31; j >= 0; --j) {
+      if (b < 0 && static_cast<int>(run + c[j]) >= need) {
+        b = lo + j;
+        ab = run;
+        inb = c[j];
+      }
+      run += c[j];
+    }
+    out[0] = b;
+    out[1] = static_cast<int>(ab);
+    out[2] = static_cast<int>(inb);
+  }
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), l));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Wave-local: penalise the not yet penalised history entries [from, cnt) of a buffer.
+__device__ __forceinline__ void fix_history(uint64_t* buf, int from, int cnt, const uint32_t* bits, float rep) {
+  const int lane = threadIdx.x & 63;
+  for (int i = from + lane; i < cnt; i += 64) {
+    const uint64_t ck = buf[i];
+    const int idx = comp_idx(ck);
+    if (bit_of(bits, idx)) {
+      const float f = penalise(key_val(comp_key(ck)), rep);
+      buf[i] = comp(key_of(__float_as_uint(f)), static_cast<uint32_t>(idx));
+    }
+  }
+  wave_lds_sync();
+}
+
+// Wave-local descending bitonic sort of buf[0..n), n padded to a power of two <= kWaveCap.
+__device__ void wave_sort_buf(uint64_t* buf, int n) {
+  const int lane = threadIdx.x & 63;
+  int p2 = 2;
+  while (p2 < n) p2 <<= 1;
+  for (int i = n + lane; i < p2; i += 64) buf[i] = 0ull;
+  wave_lds_sync();
+  for (int size = 2; size <= p2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = lane; i < (p2 >> 1); i += 64) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t x = buf[lo], y = buf[hi];
+        if ((x < y) == desc) {
+          buf[lo] = y;
+          buf[hi] = x;
+        }
+      }
+      wave_lds_sync();
+    }
+  }
+}
+
+// General rows in row mode: one pass for the row maximum / minimum (penalty in place) and the
+// penalty bitmap, which k_general then uses (as a single slice).
+__device__ void rows_general_prepass(const KArgs& a, int row, const vsmp_params& P, bool pen, const uint32_t* bits,
+                                     RowShared& sh) {
+  const int tid = threadIdx.x;
+  const int V = a.V;
+  const uint32_t* rpu = reinterpret_cast<const uint32_t*>(a.logits + static_cast<size_t>(row) * a.ld);
+  const int V4 = (V + 3) >> 2;
+  uint64_t b = 0ull;
+  uint32_t mn = 0xFFFFFFFFu;
+  for (int f = tid; f < V4; f += kRowNT) {
+    const uint4 v = *reinterpret_cast<const uint4*>(rpu + 4 * f);
+    const uint32_t x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int e = 4 * f + c;
+      if (e < V) {
+        float fv = __uint_as_float(x[c]);
+        if (pen && bit_of(bits, e)) fv = penalise(fv, P.repeat);
+        const uint32_t k = key_of(__float_as_uint(fv));
+        b = max64(b, comp(k, static_cast<uint32_t>(e)));
+        mn = min(mn, k);
+      }
+    }
+  }
+  b = block_max64<kRowNT>(b, sh.r64);
+  const uint64_t m = block_min64<kRowNT>(mn, sh.r64);
+  if (pen) {
+    const int words = (V + 31) >> 5;
+    for (int i = tid; i < words; i += kRowNT) a.s_bits[static_cast<size_t>(row) * a.words + i] = bits[i];
+  }
+  if (tid == 0) {
+    a.s_max[row] = b;
+    a.s_min[row] = static_cast<uint32_t>(m);
+  }
+}
+
+// One iteration (kRowU steps) of wave w: 16-byte groups, never past the row (4*V4 <= ld).
+__device__ __forceinline__ void row_load(const uint4* __restrict__ rp4, int V4, int it, int w, int lane,
+                                         uint4 (&buf)[kRowU]) {
+#pragma unroll
+  for (int u = 0; u < kRowU; ++u) {
+    const int g = (it * kRowU + u) * kRowW + w;
+    buf[u] = rp4[min(g * 64 + lane, V4 - 1)];
+  }
+}
+
+// Keys of step u of iteration it with validity checks (and the in-stream penalty for repeat < 1).
+// drop_hist zeroes history elements (used for the row bound, which must ignore them).
+__device__ __forceinline__ void row_keys_checked(const uint4& v, int it, int u, int w, int lane, int V, int Sw,
+                                                 bool inline_pen, bool pen, bool drop_hist, float rep,
+                                                 const uint32_t* bits, uint32_t (&kk)[4]) {
+  const int g = (it * kRowU + u) * kRowW + w;
+  const int e0 = 4 * (g * 64 + lane);
+  const bool step_ok = (it * kRowU + u) < Sw;
+  const uint32_t x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int e = e0 + c;
+    const bool ok = step_ok && e < V;
+    uint32_t bb = x[c];
+    const bool hb = (inline_pen || drop_hist) && ok && pen && bit_of(bits, e);
+    if (inline_pen && hb) bb = __float_as_uint(penalise(__uint_as_float(bb), rep));
+    uint32_t kv = key_of(bb);
+    if (drop_hist && hb) kv = 0u;
+    kk[c] = ok ? kv : 0u;
+  }
+}
+
+struct WaveState {
+  int cnt;       // entries in the wave buffer
+  int fixed;     // entries [0, fixed) carry penalised keys
+  uint32_t tw;   // the wave's own bound: keys <= tw cannot enter its top-ks
+};
+
+// Rare: the wave keeps its exact top-ks (history entries penalised first); tw becomes its ks-th
+// key. Out of line, state passed by value so the stream keeps it in registers.
+__device__ __noinline__ WaveState row_compact(uint64_t* buf, WaveState st, int ks, bool fix, const uint32_t* bits,
+                                              float rep) {
+  if (fix) fix_history(buf, st.fixed, st.cnt, bits, rep);
+  wave_sort_buf(buf, st.cnt);
+  if (st.cnt >= ks) {
+    st.cnt = ks;
+    st.tw = comp_key(buf[ks - 1]);
+  }
+  st.fixed = st.cnt;
+  return st;
+}
+
+// Appends the keys of one step that pass the filter (key >= T and key > tw) to the wave buffer.
+__device__ __forceinline__ void row_append(const uint32_t (&kk)[4], int e0, uint32_t T, uint64_t* buf, int& cnt,
+                                           int& fixed, uint32_t& tw, int ks, bool fix, const uint32_t* bits, float rep,
+                                           uint64_t lt_mask) {
+  const uint32_t gm = max(max(kk[0], kk[1]), max(kk[2], kk[3]));
+  if (__any(gm >= T && gm > tw)) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      bool pred = kk[c] >= T && kk[c] > tw;
+      uint64_t m = __ballot(pred);
+      if (m) {
+        if (cnt + 64 > kWaveCap) {
+          const WaveState st = row_compact(buf, WaveState{cnt, fixed, tw}, ks, fix, bits, rep);
+          cnt = st.cnt;
+          fixed = st.fixed;
+          tw = st.tw;
+          pred = kk[c] >= T && kk[c] > tw;
+          m = __ballot(pred);
+        }
+        if (pred) buf[cnt + __popcll(m & lt_mask)] = comp(kk[c], static_cast<uint32_t>(e0 + c));
+        cnt += __popcll(m);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void row_process(const uint4 (&cv)[kRowU], int it, int nfull, int w, int lane, int V,
+                                            int Sw, bool inline_pen, bool pen, float rep, const uint32_t* bits,
+                                            uint32_t T, uint64_t* buf, int& cnt, int& fixed, uint32_t& tw, int ks,
+                                            bool fix, uint64_t lt_mask) {
+  const bool fast = __builtin_amdgcn_readfirstlane(static_cast<int>(it < nfull && !inline_pen)) != 0;
+#pragma unroll
+  for (int u = 0; u < kRowU; ++u) {
+    uint32_t kk[4];
+    if (fast) {
+      kk[0] = key_of(cv[u].x);
+      kk[1] = key_of(cv[u].y);
+      kk[2] = key_of(cv[u].z);
+      kk[3] = key_of(cv[u].w);
+    } else {
+      row_keys_checked(cv[u], it, u, w, lane, V, Sw, inline_pen, pen, false, rep, bits, kk);
+    }
+    const int e0 = 4 * (((it * kRowU + u) * kRowW + w) * 64 + lane);
+    row_append(kk, e0, T, buf, cnt, fixed, tw, ks, fix, bits, rep, lt_mask);
+  }
+}
+
+__global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
+  __shared__ RowShared sh;
+  extern __shared__ uint32_t bits[];  // penalty bitmap of the row, ceil(V/32) words
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const vsmp_params P = row_params(a, row);
+  const int V = a.V;
+  const int path = path_of(P, V, 1);
+  const uint4* __restrict__ rp4 = reinterpret_cast<const uint4*>(a.logits + static_cast<size_t>(row) * a.ld);
+  const int V4 = (V + 3) >> 2;   // 16-byte groups
+  const int G = (V4 + 63) >> 6;  // 256-element steps of the row
+  // steps of this wave (g = s*16 + w) and its iterations of kRowU steps; wave-uniform scalars
+  const int Sw = __builtin_amdgcn_readfirstlane(w < G ? (G - w + kRowW - 1) / kRowW : 0);
+  const int nit = __builtin_amdgcn_readfirstlane((Sw + kRowU - 1) / kRowU);
+  // iterations whose every element lies inside the row (no validity checks needed)
+  const int Gfull = V >> 8;
+  const int Sfull = __builtin_amdgcn_readfirstlane(w < Gfull ? (Gfull - w + kRowW - 1) / kRowW : 0);
+  const int nfull = Sfull / kRowU;
+
+  // -- history window (scalar-loaded offsets; ids loaded before the slice)
+  int h0 = 0, h1 = 0;
+  if (a.hist_off) {
+    h0 = a.hist_off[row];
+    h1 = a.hist_off[row + 1];
+  }
+  const int H = h1 - h0;
+  const bool pen = (P.repeat != 1.0f) && H > 0;
+  const bool inline_pen = pen && !(P.repeat >= 1.0f);  // repeat < 1 raises values: penalise in the stream
+  const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
+  constexpr int HQ = 2;
+  int hid0 = -1, hid1 = -1;
+  if (pen) {
+    hid0 = a.hist[min(hfrom + tid, h1 - 1)];
+    hid1 = a.hist[min(hfrom + kRowNT + tid, h1 - 1)];
+  }
+  const int words = (V + 31) >> 5;
+
+  if (path == kPathGeneral) {
+    if (pen) {
+      for (int i = tid; i < words; i += kRowNT) bits[i] = 0u;
+      __syncthreads();
+      if (hfrom + tid < h1 && hid0 >= 0 && hid0 < V) atomicOr(&bits[hid0 >> 5], 1u << (hid0 & 31));
+      if (hfrom + kRowNT + tid < h1 && hid1 >= 0 && hid1 < V) atomicOr(&bits[hid1 >> 5], 1u << (hid1 & 31));
+      for (int i = hfrom + HQ * kRowNT + tid; i < h1; i += kRowNT) {
+        const int id = a.hist[i];
+        if (id >= 0 && id < V) atomicOr(&bits[id >> 5], 1u << (id & 31));
+      }
+    }
+    __syncthreads();
+    rows_general_prepass(a, row, P, pen, bits, sh);
+    return;
+  }
+
+  // Two iterations in flight: bA holds the even iterations, bB the odd ones. Every load is issued
+  // unconditionally (steps past the row reload its last group), so each wait below covers exactly
+  // the buffer it needs while the other buffer's loads stay in flight.
+  uint4 bA[kRowU], bB[kRowU];
+  row_load(rp4, V4, 0, w, lane, bA);
+  row_load(rp4, V4, 1, w, lane, bB);
+  for (int i = tid; i < 2 * kRowBins; i += kRowNT) (&sh.bins[0][0])[i] = 0u;
+  if (tid < kKmax) sh.rank[tid] = 0;
+  if (tid == 0) sh.ints[8] = 0;
+
+  // -- penalty bitmap (src/sampler.cpp:53-65)
+  if (pen) {
+    for (int i = tid; i < words; i += kRowNT) bits[i] = 0u;
+    __syncthreads();
+    if (hfrom + tid < h1 && hid0 >= 0 && hid0 < V) atomicOr(&bits[hid0 >> 5], 1u << (hid0 & 31));
+    if (hfrom + kRowNT + tid < h1 && hid1 >= 0 && hid1 < V) atomicOr(&bits[hid1 >> 5], 1u << (hid1 & 31));
+    for (int i = hfrom + HQ * kRowNT + tid; i < h1; i += kRowNT) {
+      const int id = a.hist[i];
+      if (id >= 0 && id < V) atomicOr(&bits[id >> 5], 1u << (id & 31));
+    }
+  }
+  __syncthreads();
+  const int k = path == kPathGreedy ? 1 : top_k_of(P, V);
+  const int ks = min(k, V);
+
+  // -- row-level lower bound T from the first iteration (history excluded)
+  uint32_t lm = 0u;
+#pragma unroll
+  for (int u = 0; u < kRowU; ++u) {
+    uint32_t kk[4];
+    row_keys_checked(bA[u], 0, u, w, lane, V, Sw, inline_pen, pen, true, P.repeat, bits, kk);
+    lm = max(lm, max(max(kk[0], kk[1]), max(kk[2], kk[3])));
+  }
+  atomicAdd(&sh.bins[0][lm >> 21], 1u);
+  __syncthreads();
+  if (w == 0) wave_find_bucket(sh.bins[0], ks, sh.ints);
+  __syncthreads();
+  const int b1 = sh.ints[0];
+  if (static_cast<int>(lm >> 21) == b1) atomicAdd(&sh.bins[1][(lm >> 10) & 2047u], 1u);
+  __syncthreads();
+  if (w == 0) wave_find_bucket(sh.bins[1], ks - sh.ints[1], sh.ints + 4);
+  __syncthreads();
+  const int b2 = sh.ints[4];
+  uint32_t T = (b1 >= 0 && b2 >= 0) ? ((static_cast<uint32_t>(b1) << 21) | (static_cast<uint32_t>(b2) << 10)) : 0u;
+  // both bin arrays start the final select cleared (ordered by the barrier after the stream)
+  for (int i = tid; i < 2 * kRowBins; i += kRowNT) (&sh.bins[0][0])[i] = 0u;
+  T = __builtin_amdgcn_readfirstlane(T);
+
+  // -- stream: append keys >= T (and > the wave's own bound tw once its buffer has compacted)
+  uint64_t* buf = sh.wbuf[w];
+  uint32_t tw = 0u;  // 0: only valid keys
+  int cnt = 0, fixed = 0;
+  const bool fix = pen && !inline_pen;
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  for (int it = 0; it < nit; it += 2) {
+    row_process(bA, it, nfull, w, lane, V, Sw, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix,
+                lt_mask);
+    row_load(rp4, V4, it + 2, w, lane, bA);
+    if (it + 1 < nit)
+      row_process(bB, it + 1, nfull, w, lane, V, Sw, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks,
+                  fix, lt_mask);
+    row_load(rp4, V4, it + 3, w, lane, bB);
+  }
+  if (fix) fix_history(buf, fixed, cnt, bits, P.repeat);
+  uint64_t wmx = 0ull;
+  for (int i = lane; i < cnt; i += 64) wmx = max64(wmx, buf[i]);
+  for (int o = 32; o > 0; o >>= 1) wmx = max64(wmx, __shfl_xor(wmx, o));
+  uint32_t np = 0;
+  if (a.info && pen) {
+    for (int i = tid; i < words; i += kRowNT) np += __popc(bits[i]);
+    for (int o = 32; o > 0; o >>= 1) np += __shfl_xor(np, o);
+  }
+  if (lane == 0) {
+    sh.wmax[w] = wmx;
+    sh.npw[w] = np;
+  }
+  __syncthreads();
+  uint64_t maxc = sh.wmax[0];
+  int n_pen = 0;
+  for (int i = 1; i < kRowW; ++i) maxc = max64(maxc, sh.wmax[i]);
+  if (a.info)
+    for (int i = 0; i < kRowW; ++i) n_pen += static_cast<int>(sh.npw[i]);
+
+  if (path == kPathGreedy) {  // src/sampler.cpp:66-70: the first maximum is the largest composite
+    if (tid == 0) {
+      const int id = comp_idx(maxc);
+      a.out[row] = id;
+      if (a.info) {
+        vsmp_row_info inf = {};
+        inf.id = id;
+        inf.path = kPathGreedy;
+        inf.k = inf.keep_minp = inf.keep = 1;
+        inf.last_id = id;
+        inf.mx = comp_val(maxc);
+        inf.n_pen = n_pen;
+        a.info[row] = inf;
+      }
+    }
+    return;
+  }
+
+  // -- exact ks-th largest composite: radix select over a shrinking window [lo, hi] of composites,
+  // 2048 buckets per pass; it ends as soon as the bucket holding the ks-th is taken whole (usually
+  // after the first pass). Penalised entries below T cannot be in the top ks and stay outside.
+  uint64_t lo = static_cast<uint64_t>(T) << 32, hi = maxc;
+  int need = ks;
+  for (int pass = 0; pass < 8; ++pass) {
+    const uint64_t R = hi - lo;
+    const int sft = R < static_cast<uint64_t>(kRowBins) ? 0 : 53 - __clzll(static_cast<long long>(R));
+    uint32_t* bins = sh.bins[pass & 1];
+    if (pass >= 1)
+      for (int i = tid; i < kRowBins; i += kRowNT) sh.bins[(pass + 1) & 1][i] = 0u;
+    for (int i = lane; i < cnt; i += 64) {
+      const uint64_t c = buf[i];
+      if (c >= lo && c <= hi) atomicAdd(&bins[(c - lo) >> sft], 1u);
+    }
+    __syncthreads();
+    if (w == 0) wave_find_bucket(bins, need, sh.ints);
+    __syncthreads();
+    const int b = sh.ints[0];
+    if (b < 0) break;  // unreachable: at least ks composites lie at or above lo
+    need -= sh.ints[1];
+    const int inb = sh.ints[2];
+    const uint64_t nlo = lo + (static_cast<uint64_t>(b) << sft);
+    const uint64_t wdt = sft == 0 ? 0ull : (1ull << sft) - 1ull;
+    hi = (hi - nlo < wdt) ? hi : nlo + wdt;
+    lo = nlo;
+    if (inb == need) break;  // the whole bucket is taken: the top ks are the composites >= lo
+  }
+
+  // -- collect the composites >= lo (exactly ks of them)
+  for (int i0 = 0; i0 < cnt; i0 += 64) {
+    const int i = i0 + lane;
+    const uint64_t c = i < cnt ? buf[i] : 0ull;
+    const bool t = i < cnt && c >= lo;
+    const uint64_t m = __ballot(t);
+    int base = 0;
+    if (lane == 0 && m) base = atomicAdd(&sh.ints[8], __popcll(m));
+    base = __shfl(base, 0);
+    if (t) {
+      const int p = base + __popcll(m & lt_mask);
+      if (p < kKmax) sh.top[p] = c;
+    }
+  }
+  __syncthreads();
+  const int nt = min(sh.ints[8], ks);
+
+  // -- sort them by rank (composites are distinct), then the reference epilogue on wave 0
+  if (nt > 64) {
+    const int parts = kRowNT / nt;  // >= 4
+    const int i = tid % nt, part = tid / nt;
+    if (part < parts) {
+      const int chunk = (nt + parts - 1) / parts;
+      const uint64_t x = sh.top[i];
+      int r = 0;
+      const int j1 = min(nt, (part + 1) * chunk);
+      for (int j = part * chunk; j < j1; ++j) r += sh.top[j] > x;
+      if (r) atomicAdd(&sh.rank[i], r);
+    }
+  }
+  if (nt > 64) __syncthreads();
+  if (w == 0) {
+    if (nt <= 64) {
+      const uint64_t x = lane < nt ? sh.top[lane] : 0ull;
+      int r = 0;
+      for (int j = 0; j < nt; ++j) r += readlane_u64(x, j) > x;
+      if (lane < nt) sh.sorted[r] = x;
+    } else {
+      for (int i = lane; i < nt; i += 64) sh.sorted[sh.rank[i]] = sh.top[i];
+    }
+    wave_lds_sync();
+    epilogue_wave(a, row, P, sh.sorted, nt, n_pen, 0);
+  }
+}
+
 }  // namespace
 
 void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st) {
@@ -1122,6 +1828,17 @@ void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st) {
 
 void launch_finish(const KArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(k_finish, dim3(a.B), dim3(kTpb), 0, st, a);
+}
+
+void launch_rows(const KArgs& a, hipStream_t st) {
+  const size_t dyn = static_cast<size_t>((a.V + 31) / 32) * sizeof(uint32_t);
+  static bool configured = false;
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_rows), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(kRowMaxDynLds));
+    configured = true;
+  }
+  hipLaunchKernelGGL(k_rows, dim3(a.B), dim3(kRowNT), dyn, st, a);
 }
 
 void launch_general(const KArgs& a, hipStream_t st) {
