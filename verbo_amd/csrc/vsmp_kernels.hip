@@ -243,6 +243,12 @@ __device__ __forceinline__ bool map_block(int b, const KArgs& a, int& row, int& 
   return row < a.B;
 }
 
+// Orders a wave's LDS writes before its later LDS reads of other lanes' entries.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
 // ---- wave-level epilogue -------------------------------------------------------------------------
 
 __device__ __forceinline__ double readlane_f64(double v, int l) {
@@ -253,42 +259,96 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
 }
 
 constexpr int kEpiJ = kKmax / 64;  // candidates per lane
+constexpr int kEpiN = kKmax + 8;    // padded length of each epilogue array
+constexpr int kEpiWs = 5 * kEpiN;   // doubles of epilogue workspace (LDS, 16-byte aligned)
+static_assert(kEpiWs <= kMergeCap, "k_finish lends its merge buffer to the epilogue");
+
+// Sequential fp64 chain x_{i+1} = x_i + v[i] (SUB: x_i - v[i]) for i in [0, roundup(n, 8)), in
+// order, over values in LDS read as wave-wide broadcasts, 8 per block (the next block's reads are
+// issued before the current block's additions). x_{i+1} is stored to out[i] by lane 0. Returns the
+// last x; v needs roundup(n, 8) + 8 readable entries.
+template <bool SUB>
+__device__ __forceinline__ double lds_chain(const double* v, int n, double x, double* out) {
+  const bool w0 = (threadIdx.x & 63) == 0;
+  const double2* v2 = reinterpret_cast<const double2*>(v);
+  double2 c0 = v2[0], c1 = v2[1], c2 = v2[2], c3 = v2[3];
+  for (int i0 = 0; i0 < n; i0 += 8) {
+    const double2* nx = v2 + (i0 >> 1) + 4;
+    const double2 n0 = nx[0], n1 = nx[1], n2 = nx[2], n3 = nx[3];
+    const double e[8] = {c0.x, c0.y, c1.x, c1.y, c2.x, c2.y, c3.x, c3.y};
+    double r[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      x = SUB ? x - e[t] : x + e[t];
+      r[t] = x;
+    }
+    if (w0) {
+      double2* o2 = reinterpret_cast<double2*>(out + i0);
+      o2[0] = make_double2(r[0], r[1]);
+      o2[1] = make_double2(r[2], r[3]);
+      o2[2] = make_double2(r[4], r[5]);
+      o2[3] = make_double2(r[6], r[7]);
+    }
+    c0 = n0;
+    c1 = n1;
+    c2 = n2;
+    c3 = n3;
+  }
+  return x;
+}
+
+// First i in [0, n) with pred(x[i]) (n when none), from values in LDS; one wave, uniform result.
+template <class F>
+__device__ __forceinline__ int lds_first(const double* x, int n, F pred) {
+  const int lane = threadIdx.x & 63;
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const int i = i0 + lane;
+    const uint64_t m = __ballot(i < n && pred(x[i]));
+    if (m) return i0 + __ffsll(static_cast<long long>(m)) - 1;
+  }
+  return n;
+}
 
 // The reference epilogue (src/sampler.cpp:79-108) run by one wave on the sorted top-k in LDS.
-// Numerators and quotients are computed one per lane; every running sum is taken in the
-// reference's sequential order by a uniform loop that reads lane values with readlane (no LDS
-// round trip per element). Called by all 64 lanes of one wave.
+// Numerators, quotients and the min-p cut are computed one element per lane; every running sum is
+// taken in the reference's sequential order by lds_chain, its running values kept in LDS, and each
+// stopping point is then found by a parallel search over them. tot (the sum of the first keep
+// numerators) is the running sum of the numerators at keep-1: the same additions in the same
+// order. ws: kEpiWs doubles of LDS. Called by all 64 lanes of one wave.
 __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsmp_params& P, const uint64_t* sorted,
-                                              int k, int n_pen, int flags) {
+                                              int k, int n_pen, int flags, double* ws) {
   const int lane = threadIdx.x & 63;
-  double pr[kEpiJ], q[kEpiJ];
+  double* s_pr = ws;               // numerators, zero past k
+  double* s_q = ws + kEpiN;        // quotients pr / sum
+  double* s_pre = ws + 2 * kEpiN;  // running sums of pr
+  double* s_acc = ws + 3 * kEpiN;  // running sums of q
+  double* s_r = ws + 4 * kEpiN;    // the draw's running remainder
+  double pr[kEpiJ];
   const float mx = comp_val(sorted[0]);
 #pragma unroll
   for (int j = 0; j < kEpiJ; ++j) {
+    pr[j] = 0.0;
     const int i = j * 64 + lane;
-    pr[j] = i < k ? numer(comp_val(sorted[i]), mx, P.temp) : 0.0;
+    if (j * 64 < k && i < k) pr[j] = numer(comp_val(sorted[i]), mx, P.temp);
+    s_pr[i] = pr[j];
   }
-  // src/sampler.cpp:84: sum in order
-  double sum = 0.0;
+  if (lane < kEpiN - kKmax) s_pr[kKmax + lane] = 0.0;
+  wave_lds_sync();
+  // src/sampler.cpp:84: sum in order (the zero numerators past k leave it unchanged)
+  const double sum = lds_chain<false>(s_pr, k, 0.0, s_pre);
 #pragma unroll
-  for (int j = 0; j < kEpiJ; ++j) {
-    const int n = min(64, k - j * 64);
-    for (int l = 0; l < n; ++l) sum += readlane_f64(pr[j], l);
-  }
-#pragma unroll
-  for (int j = 0; j < kEpiJ; ++j) q[j] = pr[j] / sum;  // the same IEEE quotient as pr[i] / sum
-  // src/sampler.cpp:86-91: keep = the first i >= 1 with pr[i] < thr (pr[0] passes when min_p <= 1)
+  for (int j = 0; j < kEpiJ; ++j) s_q[j * 64 + lane] = pr[j] / sum;  // the same IEEE quotient as pr[i] / sum
+  if (lane < kEpiN - kKmax) s_q[kKmax + lane] = 0.0;
+  // src/sampler.cpp:86-91: keep = the first i >= 1 whose pr[i] is not >= thr
   int keep = k;
   if (P.min_p > 0.0f) {
     const double thr = readlane_f64(pr[0], 0) * static_cast<double>(P.min_p);
-    keep = k;
 #pragma unroll
     for (int j = kEpiJ - 1; j >= 0; --j) {
       const int i = j * 64 + lane;
       const uint64_t fail = __ballot(i >= 1 && i < k && !(pr[j] >= thr));
       if (fail) keep = j * 64 + __ffsll(static_cast<long long>(fail)) - 1;
     }
-    // margins of the deciding comparisons
     const int kp = keep;
     double mg = 1e300;
 #pragma unroll
@@ -300,62 +360,32 @@ __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsm
     if (mg < kNearMinP) flags |= VSMP_FLAG_MINP_NEAR;
   }
   const int keep_minp = keep;
-  // src/sampler.cpp:92-100
+  wave_lds_sync();
+  // src/sampler.cpp:92-100: stop at the first i < keep whose running sum of q reaches top_p
   if (P.top_p > 0.0f && P.top_p < 1.0f) {
     const double tp = static_cast<double>(P.top_p);
-    double acc = 0.0, prev = 0.0;
-    int i = 0;
-    bool hit = false;
-#pragma unroll
-    for (int j = 0; j < kEpiJ; ++j) {
-      if (!hit) {
-        const int n = min(64, keep - j * 64);
-        for (int l = 0; l < n; ++l) {
-          prev = acc;
-          acc += readlane_f64(q[j], l);
-          if (acc >= tp) {
-            hit = true;
-            break;
-          }
-          ++i;
-        }
-      }
-    }
-    double mg = fabs(acc - tp);
-    if (i > 0) mg = fmin(mg, fabs(prev - tp));
+    lds_chain<false>(s_q, keep, 0.0, s_acc);
+    wave_lds_sync();
+    const int i = lds_first(s_acc, keep, [tp](double x) { return x >= tp; });
+    const int ia = i < keep ? i : keep - 1;
+    double mg = fabs(s_acc[ia] - tp);
+    if (i > 0) mg = fmin(mg, fabs(s_acc[i - 1] - tp));
     if (mg < kNearTopP) flags |= VSMP_FLAG_TOPP_NEAR;
     if (i + 1 < keep) keep = i + 1;
   }
   // src/sampler.cpp:101-108
-  double tot = 0.0;
-#pragma unroll
-  for (int j = 0; j < kEpiJ; ++j) {
-    const int n = min(64, keep - j * 64);
-    for (int l = 0; l < n; ++l) tot += readlane_f64(pr[j], l);
-  }
+  const double tot = s_pre[keep - 1];
   double u = 0.0;
   if (lane == 0) u = draw_u(a, row, P);
   u = readlane_f64(u, 0);
-  double r = u * tot, before = r;
-  int pick = keep - 1;
-  bool picked = false;
-#pragma unroll
-  for (int j = 0; j < kEpiJ; ++j) {
-    if (!picked) {
-      const int n = min(64, keep - j * 64);
-      for (int l = 0; l < n; ++l) {
-        before = r;
-        r -= readlane_f64(pr[j], l);
-        if (r <= 0.0) {
-          pick = j * 64 + l;
-          picked = true;
-          break;
-        }
-      }
-    }
-  }
-  double mg = fabs(r);
-  if (picked && pick > 0) mg = fmin(mg, before);
+  const double r0 = u * tot;
+  lds_chain<true>(s_pr, keep, r0, s_r);
+  wave_lds_sync();
+  const int f = lds_first(s_r, keep, [](double x) { return x <= 0.0; });
+  const bool picked = f < keep;
+  const int pick = picked ? f : keep - 1;
+  double mg = fabs(s_r[pick]);
+  if (picked && pick > 0) mg = fmin(mg, s_r[pick - 1]);
   mg = tot > 0.0 ? mg / tot : 0.0;
   if (mg < kNearDraw) flags |= VSMP_FLAG_DRAW_NEAR;
   const int id = comp_idx(sorted[pick]);
@@ -768,7 +798,7 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
 // The kernel boundary orders stage 1's slice results before these reads.
 
 __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
-  __shared__ uint64_t sm_buf[kMergeCap];
+  __shared__ __align__(16) uint64_t sm_buf[kMergeCap];
   __shared__ uint64_t sm_top[kKmax];
   __shared__ uint64_t sm_red64[kTpb / 64];
   __shared__ uint32_t sm_red32[kTpb / 64];
@@ -856,7 +886,7 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
     for (int i = tid; i < k; i += kTpb) sm_top[i] = sm_buf[i];
   }
   __syncthreads();
-  if (tid < 64) epilogue_wave(a, row, P, sm_top, k, sm_int[6], sm_int[5]);
+  if (tid < 64) epilogue_wave(a, row, P, sm_top, k, sm_int[6], sm_int[5], reinterpret_cast<double*>(sm_buf));
 }
 
 // ---- general path -------------------------------------------------------------------------------
@@ -1307,15 +1337,16 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
 
 // ---- row kernel: one workgroup streams one row (batches with at least one row per CU) -------
 //
-// Sixteen waves stream the row together (wave w takes 256-element steps w, w+16, ...), four steps
-// in flight per lane. A row-level lower bound T for the k-th largest key comes from the first
-// four steps (the k-th largest of the 1024 lane maxima, rounded down to a 22-bit prefix), so
-// after the first iteration only the few elements >= T reach a wave's LDS candidate buffer. A
-// wave whose buffer fills keeps its exact top-k (wave-local sort) and then also rejects keys not
-// above its k-th key. With repeat >= 1 a penalty can only lower a value, so the stream filters on
+// Sixteen waves stream the row together in 1024-element chunks (one 16-byte group per lane per
+// 256-element step, four steps per chunk), two chunks in flight per wave; after the first two,
+// chunks are handed out from an LDS counter. A row-level lower bound T for the k-th largest key
+// comes from the first sixteen chunks (the k-th largest of the 1024 lane maxima, rounded down to a
+// 22-bit prefix), so only the few elements >= T reach a wave's LDS candidate buffer. A wave whose
+// buffer fills keeps its exact top-k (wave-local sort) and then also rejects keys not above its
+// k-th key. With repeat >= 1 a penalty can only lower a value, so the stream filters on
 // unpenalised keys and only candidates are penalised (when a wave compacts, and at the end);
 // repeat < 1 penalises in the stream. At the end an exact radix select over the 64-bit
-// composites of every buffer gives the sorted top-k, then the reference epilogue runs.
+// composites of every buffer gives the top-k, ranked, then the reference epilogue runs on one wave.
 
 constexpr int kRowNT = 1024;
 constexpr int kRowW = kRowNT / 64;
@@ -1323,10 +1354,12 @@ constexpr int kRowU = 4;
 constexpr int kWaveCap = 512;
 constexpr int kRowBins = 2048;
 
-struct RowShared {
+static_assert(kEpiWs <= 16 * 512, "k_rows lends its candidate buffers to the epilogue");
+
+struct __align__(16) RowShared {
   uint64_t wbuf[kRowW][kWaveCap];
   uint32_t bins[2][kRowBins];  // 16-byte aligned: read as uint4 by the bucket search
-  uint64_t top[kKmax];
+  uint64_t top[kKmax + 2];
   uint64_t sorted[kKmax];
   uint64_t wmax[kRowW];
   uint64_t r64[kRowW];
@@ -1342,39 +1375,36 @@ __device__ __forceinline__ uint32_t key_of(uint32_t bits) {
   return b ^ (static_cast<uint32_t>(static_cast<int32_t>(b) >> 31) | 0x80000000u);
 }
 
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-}
-
 __device__ __forceinline__ bool bit_of(const uint32_t* bits, int e) { return (bits[e >> 5] >> (e & 31)) & 1u; }
 
+// Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts, then row broadcasts).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  int x = static_cast<int>(v);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
+  return static_cast<uint32_t>(x);
+}
+
 // One wave searches 2048 bins from the top (bucket 2047 first) for the first bucket whose running
-// count reaches `need` (such a bucket is never empty). Lane l covers buckets 2047-32l down to
-// 2016-32l. out[0] = bucket (-1 when the bins hold fewer than `need`), out[1] = count above it,
-// out[2] = its own count.
+// count reaches `need` (such a bucket is never empty). Lane l first sums buckets 2047-32l down to
+// 2016-32l; a scan over lanes finds the 32 buckets holding the crossing, and a second scan over
+// those (one per lane) the bucket. out[0] = bucket (-1 when the bins hold fewer than `need`),
+// out[1] = count above it, out[2] = its own count.
 __device__ void wave_find_bucket(const uint32_t* bins, int need, int* out) {
   const int lane = threadIdx.x & 63;
   const int lo = kRowBins - 32 * (lane + 1);
   const uint4* p = reinterpret_cast<const uint4*>(bins + lo);
-  uint32_t c[32];
+  uint32_t s = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint4 v = p[j];
-    c[4 * j] = v.x;
-    c[4 * j + 1] = v.y;
-    c[4 * j + 2] = v.z;
-    c[4 * j + 3] = v.w;
+    s += v.x + v.y + v.z + v.w;
   }
-  uint32_t s = 0;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) s += c[j];
-  uint32_t incl = s;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t t = __shfl_up(incl, o);
-    if (lane >= o) incl += t;
-  }
+  const uint32_t incl = wave_incl_scan(s);
   const uint64_t m = __ballot(static_cast<int>(incl) >= need);
   if (m == 0ull) {
     if (lane == 0) {
@@ -1384,28 +1414,18 @@ __device__ void wave_find_bucket(const uint32_t* bins, int need, int* out) {
     }
     return;
   }
-  if (lane == __ffsll(static_cast<long long>(m)) - 1) {
-    uint32_t run = incl - s, ab = 0, inb = 0;
-    int b = -1;
-#pragma unroll
-    for (int j = 31; j >= 0; --j) {
-      if (b < 0 && static_cast<int>(run + c[j]) >= need) {
-        b = lo + j;
-        ab = run;
-        inb = c[j];
-      }
-      run += c[j];
-    }
-    out[0] = b;
-    out[1] = static_cast<int>(ab);
-    out[2] = static_cast<int>(inb);
+  const int L = __ffsll(static_cast<long long>(m)) - 1;
+  const int exL = __builtin_amdgcn_readlane(static_cast<int>(incl - s), L);
+  const int loL = kRowBins - 32 * (L + 1);
+  const uint32_t c = lane < 32 ? bins[loL + 31 - lane] : 0u;
+  const uint32_t in2 = wave_incl_scan(c);
+  const uint64_t m2 = __ballot(lane < 32 && exL + static_cast<int>(in2) >= need);
+  const int t = __ffsll(static_cast<long long>(m2)) - 1;
+  if (lane == t) {
+    out[0] = loL + 31 - t;
+    out[1] = exL + static_cast<int>(in2 - c);
+    out[2] = static_cast<int>(c);
   }
-}
-
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), l));
-  return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
 // Wave-local: penalise the not yet penalised history entries [from, cnt) of a buffer.
@@ -1483,29 +1503,28 @@ __device__ void rows_general_prepass(const KArgs& a, int row, const vsmp_params&
   }
 }
 
-// One iteration (kRowU steps) of wave w: 16-byte groups, never past the row (4*V4 <= ld).
-__device__ __forceinline__ void row_load(const uint4* __restrict__ rp4, int V4, int it, int w, int lane,
+// Chunk c of the row: kRowU 256-element steps (4*kRowU KB contiguous) read by one wave in 16-byte
+// groups, never past the row (4*V4 <= ld; a chunk past the row rereads its last group).
+__device__ __forceinline__ void row_load(const uint4* __restrict__ rp4, int V4, int c, int lane,
                                          uint4 (&buf)[kRowU]) {
 #pragma unroll
   for (int u = 0; u < kRowU; ++u) {
-    const int g = (it * kRowU + u) * kRowW + w;
+    const int g = c * kRowU + u;
     buf[u] = rp4[min(g * 64 + lane, V4 - 1)];
   }
 }
 
-// Keys of step u of iteration it with validity checks (and the in-stream penalty for repeat < 1).
+// Keys of step u of chunk ch with validity checks (and the in-stream penalty for repeat < 1).
 // drop_hist zeroes history elements (used for the row bound, which must ignore them).
-__device__ __forceinline__ void row_keys_checked(const uint4& v, int it, int u, int w, int lane, int V, int Sw,
-                                                 bool inline_pen, bool pen, bool drop_hist, float rep,
-                                                 const uint32_t* bits, uint32_t (&kk)[4]) {
-  const int g = (it * kRowU + u) * kRowW + w;
-  const int e0 = 4 * (g * 64 + lane);
-  const bool step_ok = (it * kRowU + u) < Sw;
+__device__ __forceinline__ void row_keys_checked(const uint4& v, int ch, int u, int lane, int V, bool inline_pen,
+                                                 bool pen, bool drop_hist, float rep, const uint32_t* bits,
+                                                 uint32_t (&kk)[4]) {
+  const int e0 = 4 * ((ch * kRowU + u) * 64 + lane);
   const uint32_t x[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int e = e0 + c;
-    const bool ok = step_ok && e < V;
+    const bool ok = e < V;
     uint32_t bb = x[c];
     const bool hb = (inline_pen || drop_hist) && ok && pen && bit_of(bits, e);
     if (inline_pen && hb) bb = __float_as_uint(penalise(__uint_as_float(bb), rep));
@@ -1561,11 +1580,11 @@ __device__ __forceinline__ void row_append(const uint32_t (&kk)[4], int e0, uint
   }
 }
 
-__device__ __forceinline__ void row_process(const uint4 (&cv)[kRowU], int it, int nfull, int w, int lane, int V,
-                                            int Sw, bool inline_pen, bool pen, float rep, const uint32_t* bits,
-                                            uint32_t T, uint64_t* buf, int& cnt, int& fixed, uint32_t& tw, int ks,
-                                            bool fix, uint64_t lt_mask) {
-  const bool fast = __builtin_amdgcn_readfirstlane(static_cast<int>(it < nfull && !inline_pen)) != 0;
+__device__ __forceinline__ void row_process(const uint4 (&cv)[kRowU], int ch, int nfull, int lane, int V,
+                                            bool inline_pen, bool pen, float rep, const uint32_t* bits, uint32_t T,
+                                            uint64_t* buf, int& cnt, int& fixed, uint32_t& tw, int ks, bool fix,
+                                            uint64_t lt_mask) {
+  const bool fast = __builtin_amdgcn_readfirstlane(static_cast<int>(ch < nfull && !inline_pen)) != 0;
 #pragma unroll
   for (int u = 0; u < kRowU; ++u) {
     uint32_t kk[4];
@@ -1575,11 +1594,18 @@ __device__ __forceinline__ void row_process(const uint4 (&cv)[kRowU], int it, in
       kk[2] = key_of(cv[u].z);
       kk[3] = key_of(cv[u].w);
     } else {
-      row_keys_checked(cv[u], it, u, w, lane, V, Sw, inline_pen, pen, false, rep, bits, kk);
+      row_keys_checked(cv[u], ch, u, lane, V, inline_pen, pen, false, rep, bits, kk);
     }
-    const int e0 = 4 * (((it * kRowU + u) * kRowW + w) * 64 + lane);
+    const int e0 = 4 * ((ch * kRowU + u) * 64 + lane);
     row_append(kk, e0, T, buf, cnt, fixed, tw, ks, fix, bits, rep, lt_mask);
   }
+}
+
+// Next chunk id for the calling wave (wave-uniform), from the LDS counter.
+__device__ __forceinline__ int grab_chunk(int* ctr) {
+  int v = 0;
+  if ((threadIdx.x & 63) == 0) v = atomicAdd(ctr, 1);
+  return __builtin_amdgcn_readfirstlane(v);
 }
 
 __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
@@ -1591,15 +1617,10 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   const int V = a.V;
   const int path = path_of(P, V, 1);
   const uint4* __restrict__ rp4 = reinterpret_cast<const uint4*>(a.logits + static_cast<size_t>(row) * a.ld);
-  const int V4 = (V + 3) >> 2;   // 16-byte groups
-  const int G = (V4 + 63) >> 6;  // 256-element steps of the row
-  // steps of this wave (g = s*16 + w) and its iterations of kRowU steps; wave-uniform scalars
-  const int Sw = __builtin_amdgcn_readfirstlane(w < G ? (G - w + kRowW - 1) / kRowW : 0);
-  const int nit = __builtin_amdgcn_readfirstlane((Sw + kRowU - 1) / kRowU);
-  // iterations whose every element lies inside the row (no validity checks needed)
-  const int Gfull = V >> 8;
-  const int Sfull = __builtin_amdgcn_readfirstlane(w < Gfull ? (Gfull - w + kRowW - 1) / kRowW : 0);
-  const int nfull = Sfull / kRowU;
+  const int V4 = (V + 3) >> 2;                   // 16-byte groups
+  const int G = (V4 + 63) >> 6;                  // 256-element steps of the row
+  const int nch = (G + kRowU - 1) / kRowU;       // chunks of kRowU steps
+  const int nfull = V / (kRowU * 256);           // chunks whose every element lies inside the row
 
   // -- history window (scalar-loaded offsets; ids loaded before the slice)
   int h0 = 0, h1 = 0;
@@ -1639,11 +1660,18 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   // unconditionally (steps past the row reload its last group), so each wait below covers exactly
   // the buffer it needs while the other buffer's loads stay in flight.
   uint4 bA[kRowU], bB[kRowU];
-  row_load(rp4, V4, 0, w, lane, bA);
-  row_load(rp4, V4, 1, w, lane, bB);
+  // Wave w starts on chunks w and w+16; later chunks are handed out in order from an LDS counter,
+  // so the waves that get their data first take more of the row and all finish together. Each
+  // wave still sees its chunks in increasing order.
+  int cA = w, cB = w + kRowW;
+  row_load(rp4, V4, cA, lane, bA);
+  row_load(rp4, V4, cB, lane, bB);
   for (int i = tid; i < 2 * kRowBins; i += kRowNT) (&sh.bins[0][0])[i] = 0u;
   if (tid < kKmax) sh.rank[tid] = 0;
-  if (tid == 0) sh.ints[8] = 0;
+  if (tid == 0) {
+    sh.ints[8] = 0;
+    sh.ints[9] = 2 * kRowW;
+  }
 
   // -- penalty bitmap (src/sampler.cpp:53-65)
   if (pen) {
@@ -1665,7 +1693,7 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
 #pragma unroll
   for (int u = 0; u < kRowU; ++u) {
     uint32_t kk[4];
-    row_keys_checked(bA[u], 0, u, w, lane, V, Sw, inline_pen, pen, true, P.repeat, bits, kk);
+    row_keys_checked(bA[u], cA, u, lane, V, inline_pen, pen, true, P.repeat, bits, kk);
     lm = max(lm, max(max(kk[0], kk[1]), max(kk[2], kk[3])));
   }
   atomicAdd(&sh.bins[0][lm >> 21], 1u);
@@ -1689,14 +1717,16 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   int cnt = 0, fixed = 0;
   const bool fix = pen && !inline_pen;
   const uint64_t lt_mask = (1ull << lane) - 1ull;
-  for (int it = 0; it < nit; it += 2) {
-    row_process(bA, it, nfull, w, lane, V, Sw, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix,
-                lt_mask);
-    row_load(rp4, V4, it + 2, w, lane, bA);
-    if (it + 1 < nit)
-      row_process(bB, it + 1, nfull, w, lane, V, Sw, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks,
-                  fix, lt_mask);
-    row_load(rp4, V4, it + 3, w, lane, bB);
+  while (cA < nch) {  // cA < cB: a wave past the row on cA is past it on cB
+    const int nA = grab_chunk(&sh.ints[9]);
+    row_process(bA, cA, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
+    row_load(rp4, V4, nA, lane, bA);
+    const int nB = grab_chunk(&sh.ints[9]);
+    if (cB < nch)
+      row_process(bB, cB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
+    row_load(rp4, V4, nB, lane, bB);
+    cA = nA;
+    cB = nB;
   }
   if (fix) fix_history(buf, fixed, cnt, bits, P.repeat);
   uint64_t wmx = 0ull;
@@ -1798,15 +1828,21 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   if (nt > 64) __syncthreads();
   if (w == 0) {
     if (nt <= 64) {
+      if (lane == 0) sh.top[nt] = 0ull;  // pads an odd count (zero ranks below every composite)
+      wave_lds_sync();
       const uint64_t x = lane < nt ? sh.top[lane] : 0ull;
+      const ulonglong2* t2 = reinterpret_cast<const ulonglong2*>(sh.top);
       int r = 0;
-      for (int j = 0; j < nt; ++j) r += readlane_u64(x, j) > x;
+      for (int j = 0; j < nt; j += 2) {
+        const ulonglong2 y = t2[j >> 1];
+        r += (y.x > x) + (y.y > x);
+      }
       if (lane < nt) sh.sorted[r] = x;
     } else {
       for (int i = lane; i < nt; i += 64) sh.sorted[sh.rank[i]] = sh.top[i];
     }
     wave_lds_sync();
-    epilogue_wave(a, row, P, sh.sorted, nt, n_pen, 0);
+    epilogue_wave(a, row, P, sh.sorted, nt, n_pen, 0, reinterpret_cast<double*>(&sh.wbuf[0][0]));
   }
 }
 
