@@ -68,6 +68,11 @@ typedef struct {
 #define VSMP_FLAG_MINP_NEAR 2u /* a min-p comparison was within rounding distance */
 #define VSMP_FLAG_DRAW_NEAR 4u /* the draw was within 1e-6 (relative) of a CDF boundary */
 #define VSMP_FLAG_FALLBACK 8u  /* a slice needed the exact radix fallback (many near-max ties) */
+#define VSMP_FLAG_SEQ_CUTS 16u /* the top-p cut or the draw lay within 1e-12 of a boundary in the
+                                  parallel prefix sums, so both were taken from the sequential
+                                  fp64 sums instead */
+#define VSMP_FLAG_CUTS_DIFFER 32u /* diagnostics only (info requested): the parallel decision and
+                                     the sequential one differed; never expected */
 
 typedef struct vsmp_ctx vsmp_ctx;
 

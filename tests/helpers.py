@@ -87,6 +87,8 @@ class Run:
             near += int(draw_amb)
             if g["id"] != self.ids[r]:
                 problems.append(f"row {r}: out {self.ids[r]} != info.id {g['id']}")
+            if g["flags"] & V.FLAG_CUTS_DIFFER:
+                problems.append(f"row {r}: parallel and sequential cuts differ")
             if o["greedy"]:
                 if self.ids[r] != self.o_ids[r]:
                     problems.append(f"row {r}: greedy id {self.ids[r]} != oracle {self.o_ids[r]}")

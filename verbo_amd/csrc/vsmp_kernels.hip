@@ -309,20 +309,129 @@ __device__ __forceinline__ int lds_first(const double* x, int n, F pred) {
   return n;
 }
 
-// The reference epilogue (src/sampler.cpp:79-108) run by one wave on the sorted top-k in LDS.
-// Numerators, quotients and the min-p cut are computed one element per lane; every running sum is
-// taken in the reference's sequential order by lds_chain, its running values kept in LDS, and each
-// stopping point is then found by a parallel search over them. tot (the sum of the first keep
-// numerators) is the running sum of the numerators at keep-1: the same additions in the same
-// order. ws: kEpiWs doubles of LDS. Called by all 64 lanes of one wave.
-__device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsmp_params& P, const uint64_t* sorted,
-                                              int k, int n_pen, int flags, double* ws) {
+template <int CTRL, int RM>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(b), CTRL, RM, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), CTRL, RM, 0xf, false);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<uint32_t>(lo));
+}
+
+// Inclusive prefix sum of doubles over the 64 lanes of a wave (a tree order, not the sequential one).
+__device__ __forceinline__ double wave_incl_scan_f64(double v) {
+  v += dpp_f64<0x111, 0xf>(v);
+  v += dpp_f64<0x112, 0xf>(v);
+  v += dpp_f64<0x114, 0xf>(v);
+  v += dpp_f64<0x118, 0xf>(v);
+  v += dpp_f64<0x142, 0xa>(v);
+  v += dpp_f64<0x143, 0xc>(v);
+  return v;
+}
+
+// Element i of a per-lane array (slot i / 64, lane i % 64); i uniform.
+__device__ __forceinline__ double elem_at(const double (&x)[kEpiJ], int i) {
+  double r = 0.0;
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j)
+    if ((i >> 6) == j) r = readlane_f64(x[j], i & 63);
+  return r;
+}
+
+// Inclusive prefix sums of a per-lane array over elements [0, n), slot by slot.
+__device__ __forceinline__ void prefix_f64(const double (&x)[kEpiJ], int n, double (&out)[kEpiJ]) {
+  double carry = 0.0;
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j) {
+    out[j] = 0.0;
+    if (j * 64 < n) {
+      out[j] = wave_incl_scan_f64(x[j]) + carry;
+      carry = readlane_f64(out[j], 63);
+    }
+  }
+}
+
+// First i in [0, n) with pred(x[i]) over a per-lane array (n when none); uniform.
+template <class F>
+__device__ __forceinline__ int first_where(const double (&x)[kEpiJ], int n, F pred) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j) {
+    const uint64_t m = __ballot(j * 64 + lane < n && pred(x[j]));
+    if (m) return j * 64 + __ffsll(static_cast<long long>(m)) - 1;
+  }
+  return n;
+}
+
+constexpr double kCutDelta = 1e-12;  // the parallel sums decide a cut only with this much room
+
+struct Cuts {
+  int keep;     // draw set size after top-p
+  int pick;     // sorted position drawn
+  int flags;
+  double sum, tot, mg;
+};
+
+// The reference's top-p cut and draw (src/sampler.cpp:84-108) in its sequential fp64 order: each
+// running sum is taken by lds_chain, its running values kept in LDS, and every stopping point is
+// then found by a parallel search over them. tot (the sum of the first keep numerators) is the
+// running sum of the numerators at keep-1: the same additions in the same order.
+__device__ __forceinline__ Cuts cuts_sequential(const vsmp_params& P, const double (&pr)[kEpiJ], int k, int keep,
+                                                double u, double* ws) {
   const int lane = threadIdx.x & 63;
   double* s_pr = ws;               // numerators, zero past k
   double* s_q = ws + kEpiN;        // quotients pr / sum
   double* s_pre = ws + 2 * kEpiN;  // running sums of pr
   double* s_acc = ws + 3 * kEpiN;  // running sums of q
   double* s_r = ws + 4 * kEpiN;    // the draw's running remainder
+  Cuts c;
+  c.flags = 0;
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j) s_pr[j * 64 + lane] = pr[j];
+  if (lane < kEpiN - kKmax) {
+    s_pr[kKmax + lane] = 0.0;
+    s_q[kKmax + lane] = 0.0;
+  }
+  wave_lds_sync();
+  c.sum = lds_chain<false>(s_pr, k, 0.0, s_pre);  // the zero numerators past k leave it unchanged
+#pragma unroll
+  for (int j = 0; j < kEpiJ; ++j) s_q[j * 64 + lane] = pr[j] / c.sum;  // the IEEE quotient pr[i] / sum
+  wave_lds_sync();
+  if (P.top_p > 0.0f && P.top_p < 1.0f) {
+    const double tp = static_cast<double>(P.top_p);
+    lds_chain<false>(s_q, keep, 0.0, s_acc);
+    wave_lds_sync();
+    const int i = lds_first(s_acc, keep, [tp](double x) { return x >= tp; });
+    const int ia = i < keep ? i : keep - 1;
+    double mg = fabs(s_acc[ia] - tp);
+    if (i > 0) mg = fmin(mg, fabs(s_acc[i - 1] - tp));
+    if (mg < kNearTopP) c.flags |= VSMP_FLAG_TOPP_NEAR;
+    if (i + 1 < keep) keep = i + 1;
+  }
+  c.keep = keep;
+  c.tot = s_pre[keep - 1];
+  lds_chain<true>(s_pr, keep, u * c.tot, s_r);
+  wave_lds_sync();
+  const int f = lds_first(s_r, keep, [](double x) { return x <= 0.0; });
+  c.pick = f < keep ? f : keep - 1;
+  double mg = fabs(s_r[c.pick]);
+  if (f < keep && f > 0) mg = fmin(mg, s_r[f - 1]);
+  c.mg = c.tot > 0.0 ? mg / c.tot : 0.0;
+  if (c.mg < kNearDraw) c.flags |= VSMP_FLAG_DRAW_NEAR;
+  return c;
+}
+
+// The reference epilogue (src/sampler.cpp:79-108) run by one wave on the sorted top-k in LDS.
+// Numerators and the min-p cut are computed one element per lane, exactly. The top-p cut and the
+// draw are first decided from one parallel prefix sum of the numerators (DPP scans): a sum of at
+// most 256 non-negative terms in any order lies within 256 * 2^-52 (relative) of the sequential
+// one, and the reference's running sum of q = pr / sum within as much of (running sum of pr) /
+// sum, so a decision whose prefix sums clear the boundary by kCutDelta (relative to the sum) is
+// the one the sequential sums take. Otherwise, and whenever row diagnostics are requested, the
+// sequential sums are taken as well (cuts_sequential); they decide whenever the parallel sums
+// could not. ws: kEpiWs doubles of LDS. Called by all 64 lanes of one wave.
+__device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsmp_params& P, const uint64_t* sorted,
+                                              int k, int n_pen, int flags, double u, double* ws) {
+  const int lane = threadIdx.x & 63;
   double pr[kEpiJ];
   const float mx = comp_val(sorted[0]);
 #pragma unroll
@@ -330,15 +439,7 @@ __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsm
     pr[j] = 0.0;
     const int i = j * 64 + lane;
     if (j * 64 < k && i < k) pr[j] = numer(comp_val(sorted[i]), mx, P.temp);
-    s_pr[i] = pr[j];
   }
-  if (lane < kEpiN - kKmax) s_pr[kKmax + lane] = 0.0;
-  wave_lds_sync();
-  // src/sampler.cpp:84: sum in order (the zero numerators past k leave it unchanged)
-  const double sum = lds_chain<false>(s_pr, k, 0.0, s_pre);
-#pragma unroll
-  for (int j = 0; j < kEpiJ; ++j) s_q[j * 64 + lane] = pr[j] / sum;  // the same IEEE quotient as pr[i] / sum
-  if (lane < kEpiN - kKmax) s_q[kKmax + lane] = 0.0;
   // src/sampler.cpp:86-91: keep = the first i >= 1 whose pr[i] is not >= thr
   int keep = k;
   if (P.min_p > 0.0f) {
@@ -349,46 +450,70 @@ __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsm
       const uint64_t fail = __ballot(i >= 1 && i < k && !(pr[j] >= thr));
       if (fail) keep = j * 64 + __ffsll(static_cast<long long>(fail)) - 1;
     }
-    const int kp = keep;
-    double mg = 1e300;
-#pragma unroll
-    for (int j = 0; j < kEpiJ; ++j) {
-      const int i = j * 64 + lane;
-      if ((i == kp - 1 || i == kp) && i < k) mg = fmin(mg, fabs(pr[j] - thr) / thr);
-    }
-    for (int o = 32; o > 0; o >>= 1) mg = fmin(mg, __shfl_xor(mg, o));
-    if (mg < kNearMinP) flags |= VSMP_FLAG_MINP_NEAR;
+    bool near = fabs(elem_at(pr, keep - 1) - thr) < kNearMinP * thr;
+    if (keep < k) near = near || fabs(elem_at(pr, keep) - thr) < kNearMinP * thr;
+    if (near) flags |= VSMP_FLAG_MINP_NEAR;
   }
   const int keep_minp = keep;
-  wave_lds_sync();
-  // src/sampler.cpp:92-100: stop at the first i < keep whose running sum of q reaches top_p
-  if (P.top_p > 0.0f && P.top_p < 1.0f) {
-    const double tp = static_cast<double>(P.top_p);
-    lds_chain<false>(s_q, keep, 0.0, s_acc);
-    wave_lds_sync();
-    const int i = lds_first(s_acc, keep, [tp](double x) { return x >= tp; });
-    const int ia = i < keep ? i : keep - 1;
-    double mg = fabs(s_acc[ia] - tp);
-    if (i > 0) mg = fmin(mg, fabs(s_acc[i - 1] - tp));
-    if (mg < kNearTopP) flags |= VSMP_FLAG_TOPP_NEAR;
-    if (i + 1 < keep) keep = i + 1;
+
+  // -- parallel decision
+  Cuts f;
+  f.flags = 0;
+  bool ok = true;
+  {
+    double S[kEpiJ];
+    prefix_f64(pr, k, S);
+    f.sum = elem_at(S, k - 1);
+    int kf = keep;
+    if (P.top_p > 0.0f && P.top_p < 1.0f) {
+      // the running sum of q = pr / sum reaches top_p where the running sum of pr reaches top_p * sum
+      const double thr = static_cast<double>(P.top_p) * f.sum;
+      const double band = kCutDelta * f.sum;
+      const int i = first_where(S, kf, [thr](double x) { return x >= thr; });
+      const double si = elem_at(S, i < kf ? i : kf - 1);
+      const double sp = i > 0 ? elem_at(S, i - 1) : 0.0;
+      if (i < kf) ok = ok && (si - thr > band) && (i == 0 || thr - sp > band);
+      else ok = ok && (thr - si > band);
+      double mg = fabs(si - thr);
+      if (i > 0) mg = fmin(mg, fabs(sp - thr));
+      if (mg < kNearTopP * f.sum) f.flags |= VSMP_FLAG_TOPP_NEAR;
+      if (i + 1 < kf) kf = i + 1;
+    }
+    f.keep = kf;
+    f.tot = elem_at(S, kf - 1);
+    const double r0 = u * f.tot;
+    double D[kEpiJ];
+#pragma unroll
+    for (int j = 0; j < kEpiJ; ++j) D[j] = r0 - S[j];
+    const int i = first_where(D, kf, [](double x) { return x <= 0.0; });
+    const double band = kCutDelta * f.tot;
+    const double di = elem_at(D, i < kf ? i : kf - 1);
+    const double dp = i > 0 ? elem_at(D, i - 1) : r0;
+    if (i < kf) ok = ok && (-di > band) && (i == 0 || dp > band);
+    else ok = ok && (di > band);
+    ok = ok && f.tot > 0.0;
+    f.pick = i < kf ? i : kf - 1;
+    double mg = fabs(di);
+    if (i < kf && i > 0) mg = fmin(mg, dp);
+    f.mg = f.tot > 0.0 ? mg / f.tot : 0.0;
+    if (f.mg < kNearDraw) f.flags |= VSMP_FLAG_DRAW_NEAR;
   }
-  // src/sampler.cpp:101-108
-  const double tot = s_pre[keep - 1];
-  double u = 0.0;
-  if (lane == 0) u = draw_u(a, row, P);
-  u = readlane_f64(u, 0);
-  const double r0 = u * tot;
-  lds_chain<true>(s_pr, keep, r0, s_r);
-  wave_lds_sync();
-  const int f = lds_first(s_r, keep, [](double x) { return x <= 0.0; });
-  const bool picked = f < keep;
-  const int pick = picked ? f : keep - 1;
-  double mg = fabs(s_r[pick]);
-  if (picked && pick > 0) mg = fmin(mg, s_r[pick - 1]);
-  mg = tot > 0.0 ? mg / tot : 0.0;
-  if (mg < kNearDraw) flags |= VSMP_FLAG_DRAW_NEAR;
-  const int id = comp_idx(sorted[pick]);
+  Cuts c = f;
+  if (!ok || a.info) {
+    const Cuts e = cuts_sequential(P, pr, k, keep, u, ws);
+    if (!ok) {
+      c = e;
+      c.flags |= VSMP_FLAG_SEQ_CUTS;
+    } else {
+      if (e.keep != f.keep || e.pick != f.pick) c.flags |= VSMP_FLAG_CUTS_DIFFER;
+      c.flags = (c.flags & VSMP_FLAG_CUTS_DIFFER) | e.flags;
+      c.sum = e.sum;
+      c.tot = e.tot;
+      c.mg = e.mg;
+    }
+  }
+  flags |= c.flags;
+  const int id = comp_idx(sorted[c.pick]);
   if (lane == 0) {
     a.out[row] = id;
     if (a.info) {
@@ -397,21 +522,21 @@ __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsm
       inf.path = kPathSmallK;
       inf.k = k;
       inf.keep_minp = keep_minp;
-      inf.keep = keep;
-      inf.rank = pick;
-      inf.last_id = comp_idx(sorted[keep - 1]);
+      inf.keep = c.keep;
+      inf.rank = c.pick;
+      inf.last_id = comp_idx(sorted[c.keep - 1]);
       inf.flags = flags;
       inf.mx = mx;
       inf.n_pen = n_pen;
-      inf.sum = sum;
-      inf.tot = tot;
+      inf.sum = c.sum;
+      inf.tot = c.tot;
       inf.u = u;
-      inf.draw_margin = mg;
+      inf.draw_margin = c.mg;
       a.info[row] = inf;
     }
   }
   if (a.cand_ids && a.cand_cap > 0) {
-    const int m = min(keep, a.cand_cap);
+    const int m = min(c.keep, a.cand_cap);
 #pragma unroll
     for (int j = 0; j < kEpiJ; ++j) {
       const int i = j * 64 + lane;
@@ -886,7 +1011,11 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
     for (int i = tid; i < k; i += kTpb) sm_top[i] = sm_buf[i];
   }
   __syncthreads();
-  if (tid < 64) epilogue_wave(a, row, P, sm_top, k, sm_int[6], sm_int[5], reinterpret_cast<double*>(sm_buf));
+  if (tid < 64) {
+    double u = 0.0;
+    if (tid == 0) u = draw_u(a, row, P);
+    epilogue_wave(a, row, P, sm_top, k, sm_int[6], sm_int[5], readlane_f64(u, 0), reinterpret_cast<double*>(sm_buf));
+  }
 }
 
 // ---- general path -------------------------------------------------------------------------------
@@ -1359,12 +1488,11 @@ static_assert(kEpiWs <= 16 * 512, "k_rows lends its candidate buffers to the epi
 struct __align__(16) RowShared {
   uint64_t wbuf[kRowW][kWaveCap];
   uint32_t bins[2][kRowBins];  // 16-byte aligned: read as uint4 by the bucket search
-  uint64_t top[kKmax + 2];
   uint64_t sorted[kKmax];
+  uint64_t top[kKmax];
   uint64_t wmax[kRowW];
   uint64_t r64[kRowW];
   int rank[kKmax];
-  int cnt[kRowW];
   uint32_t npw[kRowW];
   int ints[16];
 };
@@ -1639,6 +1767,8 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     hid1 = a.hist[min(hfrom + kRowNT + tid, h1 - 1)];
   }
   const int words = (V + 31) >> 5;
+  double u0 = 0.0;  // the draw, taken early (thread 0) so that it is off the epilogue's path
+  if (tid == 0 && path == kPathSmallK) u0 = draw_u(a, row, P);
 
   if (path == kPathGeneral) {
     if (pen) {
@@ -1656,14 +1786,14 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     return;
   }
 
-  // Two iterations in flight: bA holds the even iterations, bB the odd ones. Every load is issued
-  // unconditionally (steps past the row reload its last group), so each wait below covers exactly
-  // the buffer it needs while the other buffer's loads stay in flight.
+  // Two chunks in flight per wave, in bA and bB. Every load is issued unconditionally (a chunk past
+  // the row rereads its last group), so each wait below covers exactly the buffer it needs while
+  // the other buffer's loads stay in flight. Wave w starts on chunks w and w+16; later chunks are
+  // handed out in order from an LDS counter, so the waves that get their data first take more of
+  // the row and all finish together. Each wave sees its chunks in increasing order.
   uint4 bA[kRowU], bB[kRowU];
-  // Wave w starts on chunks w and w+16; later chunks are handed out in order from an LDS counter,
-  // so the waves that get their data first take more of the row and all finish together. Each
-  // wave still sees its chunks in increasing order.
-  int cA = w, cB = w + kRowW;
+  const int c0 = w;
+  int cA = c0, cB = w + kRowW;
   row_load(rp4, V4, cA, lane, bA);
   row_load(rp4, V4, cB, lane, bB);
   for (int i = tid; i < 2 * kRowBins; i += kRowNT) (&sh.bins[0][0])[i] = 0u;
@@ -1688,14 +1818,21 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   const int k = path == kPathGreedy ? 1 : top_k_of(P, V);
   const int ks = min(k, V);
 
-  // -- row-level lower bound T from the first iteration (history excluded)
+  // -- row-level lower bound T from the first sixteen chunks (history excluded). The first chunk
+  // is parked in the wave's (still empty) candidate buffer and the next one put in flight before
+  // the bound's barriers, so the row keeps streaming meanwhile.
   uint32_t lm = 0u;
 #pragma unroll
   for (int u = 0; u < kRowU; ++u) {
     uint32_t kk[4];
-    row_keys_checked(bA[u], cA, u, lane, V, inline_pen, pen, true, P.repeat, bits, kk);
+    row_keys_checked(bA[u], c0, u, lane, V, inline_pen, pen, true, P.repeat, bits, kk);
     lm = max(lm, max(max(kk[0], kk[1]), max(kk[2], kk[3])));
   }
+  uint4* park = reinterpret_cast<uint4*>(sh.wbuf[w]);  // kRowU * 64 groups = the wave's 4 KB
+#pragma unroll
+  for (int u = 0; u < kRowU; ++u) park[u * 64 + lane] = bA[u];
+  cA = grab_chunk(&sh.ints[9]);
+  row_load(rp4, V4, cA, lane, bA);
   atomicAdd(&sh.bins[0][lm >> 21], 1u);
   __syncthreads();
   if (w == 0) wave_find_bucket(sh.bins[0], ks, sh.ints);
@@ -1707,9 +1844,9 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   __syncthreads();
   const int b2 = sh.ints[4];
   uint32_t T = (b1 >= 0 && b2 >= 0) ? ((static_cast<uint32_t>(b1) << 21) | (static_cast<uint32_t>(b2) << 10)) : 0u;
+  T = __builtin_amdgcn_readfirstlane(T);
   // both bin arrays start the final select cleared (ordered by the barrier after the stream)
   for (int i = tid; i < 2 * kRowBins; i += kRowNT) (&sh.bins[0][0])[i] = 0u;
-  T = __builtin_amdgcn_readfirstlane(T);
 
   // -- stream: append keys >= T (and > the wave's own bound tw once its buffer has compacted)
   uint64_t* buf = sh.wbuf[w];
@@ -1717,16 +1854,24 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   int cnt = 0, fixed = 0;
   const bool fix = pen && !inline_pen;
   const uint64_t lt_mask = (1ull << lane) - 1ull;
-  while (cA < nch) {  // cA < cB: a wave past the row on cA is past it on cB
-    const int nA = grab_chunk(&sh.ints[9]);
-    row_process(bA, cA, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
-    row_load(rp4, V4, nA, lane, bA);
+  {
+    uint4 pk[kRowU];  // the parked chunk, read back whole before its appends reuse the buffer
+#pragma unroll
+    for (int u = 0; u < kRowU; ++u) pk[u] = park[u * 64 + lane];
+    wave_lds_sync();
+    if (c0 < nch)
+      row_process(pk, c0, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
+  }
+  while (cB < nch) {  // cB < cA: a wave past the row on cB is past it on cA
     const int nB = grab_chunk(&sh.ints[9]);
-    if (cB < nch)
-      row_process(bB, cB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
+    row_process(bB, cB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
     row_load(rp4, V4, nB, lane, bB);
-    cA = nA;
+    const int nA = grab_chunk(&sh.ints[9]);
+    if (cA < nch)
+      row_process(bA, cA, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
+    row_load(rp4, V4, nA, lane, bA);
     cB = nB;
+    cA = nA;
   }
   if (fix) fix_history(buf, fixed, cnt, bits, P.repeat);
   uint64_t wmx = 0ull;
@@ -1743,9 +1888,9 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   }
   __syncthreads();
   uint64_t maxc = sh.wmax[0];
-  int n_pen = 0;
   for (int i = 1; i < kRowW; ++i) maxc = max64(maxc, sh.wmax[i]);
-  if (a.info)
+  int n_pen = 0;
+  if (a.info && w == 0)
     for (int i = 0; i < kRowW; ++i) n_pen += static_cast<int>(sh.npw[i]);
 
   if (path == kPathGreedy) {  // src/sampler.cpp:66-70: the first maximum is the largest composite
@@ -1824,17 +1969,18 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
       for (int j = part * chunk; j < j1; ++j) r += sh.top[j] > x;
       if (r) atomicAdd(&sh.rank[i], r);
     }
+    __syncthreads();
   }
-  if (nt > 64) __syncthreads();
   if (w == 0) {
     if (nt <= 64) {
-      if (lane == 0) sh.top[nt] = 0ull;  // pads an odd count (zero ranks below every composite)
+      if (lane >= nt) sh.top[lane] = 0ull;  // zero ranks below every composite
       wave_lds_sync();
-      const uint64_t x = lane < nt ? sh.top[lane] : 0ull;
+      const uint64_t x = sh.top[lane];
       const ulonglong2* t2 = reinterpret_cast<const ulonglong2*>(sh.top);
       int r = 0;
-      for (int j = 0; j < nt; j += 2) {
-        const ulonglong2 y = t2[j >> 1];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const ulonglong2 y = t2[j];
         r += (y.x > x) + (y.y > x);
       }
       if (lane < nt) sh.sorted[r] = x;
@@ -1842,7 +1988,7 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
       for (int i = lane; i < nt; i += 64) sh.sorted[sh.rank[i]] = sh.top[i];
     }
     wave_lds_sync();
-    epilogue_wave(a, row, P, sh.sorted, nt, n_pen, 0, reinterpret_cast<double*>(&sh.wbuf[0][0]));
+    epilogue_wave(a, row, P, sh.sorted, nt, n_pen, 0, readlane_f64(u0, 0), reinterpret_cast<double*>(&sh.wbuf[0][0]));
   }
 }
 
