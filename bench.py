@@ -85,6 +85,9 @@ def main():
     ap.add_argument("--workload", default="peaked", choices=sorted(DESCR))
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0: skip)")
     ap.add_argument("--min-buffer-mb", type=float, default=640.0)
+    ap.add_argument("--copy", action="store_true",
+                    help="time a plain device copy of one logits buffer per step instead (the known-size kernel "
+                         "that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the sampler has no multi-GPU path in this build (asked for "
@@ -117,6 +120,12 @@ def main():
     def step(i):
         ctx.pick_batch(bufs[i % nbuf], params, hist, hoff, V.U_COUNTER, counter=i, out=out, stream=stream)
 
+    if args.copy:
+        dst = torch.empty_like(bufs[0])
+
+        def step(i):  # noqa: F811 - the calibration step replaces the sampler step
+            dst.copy_(bufs[i % nbuf])
+
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -135,6 +144,11 @@ def main():
     ms_per_step = total_ms / args.steps
     log(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (median {sorted(per)[len(per) // 2] * 1e3:.1f} "
         f"us, wall {wall:.3f}s)")
+    if args.copy:
+        gbs = 2 * nbytes / (ms_per_step * 1e-3) / 1e9
+        print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "us_per_copy": ms_per_step * 1e3,
+                          "GB_per_s_read_plus_write": gbs}), flush=True)
+        return
     alg = w.algorithmic_bytes()
     achieved = alg / (ms_per_step * 1e-3) / 1e9
     traffic = traffic_from_profiles(args.workload)

@@ -73,7 +73,7 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {  // SplitMix64 output fu
 }
 
 // One draw for a non-greedy row (called by exactly one thread per row and call).
-__device__ double draw_u(const KArgs& a, int row, const vsmp_params& p) {
+__device__ __forceinline__ double draw_u(const KArgs& a, int row, const vsmp_params& p) {
   if (a.u_mode == VSMP_U_SUPPLIED) return a.u[row];
   if (a.u_mode == VSMP_U_COUNTER) {
     // row r's stream is seeded with its own params.seed, or with seed + r when all rows share one
@@ -261,7 +261,7 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
 constexpr int kEpiJ = kKmax / 64;  // candidates per lane
 constexpr int kEpiN = kKmax + 8;    // padded length of each epilogue array
 constexpr int kEpiWs = 5 * kEpiN;   // doubles of epilogue workspace (LDS, 16-byte aligned)
-static_assert(kEpiWs <= kMergeCap, "k_finish lends its merge buffer to the epilogue");
+static_assert(kEpiWs + kKmax <= kMergeCap, "k_finish lends its merge buffer to the epilogue");
 
 // Sequential fp64 chain x_{i+1} = x_i + v[i] (SUB: x_i - v[i]) for i in [0, roundup(n, 8)), in
 // order, over values in LDS read as wave-wide broadcasts, 8 per block (the next block's reads are
@@ -328,20 +328,27 @@ __device__ __forceinline__ double wave_incl_scan_f64(double v) {
   return v;
 }
 
-// Element i of a per-lane array (slot i / 64, lane i % 64); i uniform.
-__device__ __forceinline__ double elem_at(const double (&x)[kEpiJ], int i) {
+// Element i of a per-lane array of J slots (slot i / 64, lane i % 64); i uniform.
+template <int J>
+__device__ __forceinline__ double elem_at(const double (&x)[J], int i) {
+  if (J == 1) return readlane_f64(x[0], i & 63);
   double r = 0.0;
 #pragma unroll
-  for (int j = 0; j < kEpiJ; ++j)
+  for (int j = 0; j < J; ++j)
     if ((i >> 6) == j) r = readlane_f64(x[j], i & 63);
   return r;
 }
 
 // Inclusive prefix sums of a per-lane array over elements [0, n), slot by slot.
-__device__ __forceinline__ void prefix_f64(const double (&x)[kEpiJ], int n, double (&out)[kEpiJ]) {
+template <int J>
+__device__ __forceinline__ void prefix_f64(const double (&x)[J], int n, double (&out)[J]) {
+  if (J == 1) {
+    out[0] = wave_incl_scan_f64(x[0]);
+    return;
+  }
   double carry = 0.0;
 #pragma unroll
-  for (int j = 0; j < kEpiJ; ++j) {
+  for (int j = 0; j < J; ++j) {
     out[j] = 0.0;
     if (j * 64 < n) {
       out[j] = wave_incl_scan_f64(x[j]) + carry;
@@ -351,11 +358,11 @@ __device__ __forceinline__ void prefix_f64(const double (&x)[kEpiJ], int n, doub
 }
 
 // First i in [0, n) with pred(x[i]) over a per-lane array (n when none); uniform.
-template <class F>
-__device__ __forceinline__ int first_where(const double (&x)[kEpiJ], int n, F pred) {
+template <int J, class F>
+__device__ __forceinline__ int first_where(const double (&x)[J], int n, F pred) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int j = 0; j < kEpiJ; ++j) {
+  for (int j = 0; j < J; ++j) {
     const uint64_t m = __ballot(j * 64 + lane < n && pred(x[j]));
     if (m) return j * 64 + __ffsll(static_cast<long long>(m)) - 1;
   }
@@ -375,8 +382,8 @@ struct Cuts {
 // running sum is taken by lds_chain, its running values kept in LDS, and every stopping point is
 // then found by a parallel search over them. tot (the sum of the first keep numerators) is the
 // running sum of the numerators at keep-1: the same additions in the same order.
-__device__ __forceinline__ Cuts cuts_sequential(const vsmp_params& P, const double (&pr)[kEpiJ], int k, int keep,
-                                                double u, double* ws) {
+// Out of line: it runs only with row diagnostics or next to a boundary. spr: the k numerators.
+__device__ __noinline__ Cuts cuts_sequential(float top_p, const double* spr, int k, int keep, double u, double* ws) {
   const int lane = threadIdx.x & 63;
   double* s_pr = ws;               // numerators, zero past k
   double* s_q = ws + kEpiN;        // quotients pr / sum
@@ -385,8 +392,13 @@ __device__ __forceinline__ Cuts cuts_sequential(const vsmp_params& P, const doub
   double* s_r = ws + 4 * kEpiN;    // the draw's running remainder
   Cuts c;
   c.flags = 0;
+  double pr[kEpiJ];
 #pragma unroll
-  for (int j = 0; j < kEpiJ; ++j) s_pr[j * 64 + lane] = pr[j];
+  for (int j = 0; j < kEpiJ; ++j) {
+    const int i = j * 64 + lane;
+    pr[j] = i < k ? spr[i] : 0.0;
+    s_pr[i] = pr[j];
+  }
   if (lane < kEpiN - kKmax) {
     s_pr[kKmax + lane] = 0.0;
     s_q[kKmax + lane] = 0.0;
@@ -396,8 +408,8 @@ __device__ __forceinline__ Cuts cuts_sequential(const vsmp_params& P, const doub
 #pragma unroll
   for (int j = 0; j < kEpiJ; ++j) s_q[j * 64 + lane] = pr[j] / c.sum;  // the IEEE quotient pr[i] / sum
   wave_lds_sync();
-  if (P.top_p > 0.0f && P.top_p < 1.0f) {
-    const double tp = static_cast<double>(P.top_p);
+  if (top_p > 0.0f && top_p < 1.0f) {
+    const double tp = static_cast<double>(top_p);
     lds_chain<false>(s_q, keep, 0.0, s_acc);
     wave_lds_sync();
     const int i = lds_first(s_acc, keep, [tp](double x) { return x >= tp; });
@@ -420,8 +432,9 @@ __device__ __forceinline__ Cuts cuts_sequential(const vsmp_params& P, const doub
   return c;
 }
 
-// The reference epilogue (src/sampler.cpp:79-108) run by one wave on the sorted top-k in LDS.
-// Numerators and the min-p cut are computed one element per lane, exactly. The top-p cut and the
+// The reference epilogue (src/sampler.cpp:79-108) run by one wave on the sorted top-k in LDS and
+// its numerators spr (src/sampler.cpp:79-83, computed by the caller). The min-p cut is computed
+// one element per lane, exactly. The top-p cut and the
 // draw are first decided from one parallel prefix sum of the numerators (DPP scans): a sum of at
 // most 256 non-negative terms in any order lies within 256 * 2^-52 (relative) of the sequential
 // one, and the reference's running sum of q = pr / sum within as much of (running sum of pr) /
@@ -429,23 +442,25 @@ __device__ __forceinline__ Cuts cuts_sequential(const vsmp_params& P, const doub
 // the one the sequential sums take. Otherwise, and whenever row diagnostics are requested, the
 // sequential sums are taken as well (cuts_sequential); they decide whenever the parallel sums
 // could not. ws: kEpiWs doubles of LDS. Called by all 64 lanes of one wave.
+// J: slots per lane (k <= 64 J).
+template <int J>
 __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsmp_params& P, const uint64_t* sorted,
-                                              int k, int n_pen, int flags, double u, double* ws) {
+                                              const double* spr, int k, int n_pen, int flags, double u, double* ws) {
   const int lane = threadIdx.x & 63;
-  double pr[kEpiJ];
+  double pr[J];
   const float mx = comp_val(sorted[0]);
 #pragma unroll
-  for (int j = 0; j < kEpiJ; ++j) {
+  for (int j = 0; j < J; ++j) {
     pr[j] = 0.0;
     const int i = j * 64 + lane;
-    if (j * 64 < k && i < k) pr[j] = numer(comp_val(sorted[i]), mx, P.temp);
+    if (j * 64 < k && i < k) pr[j] = spr[i];
   }
   // src/sampler.cpp:86-91: keep = the first i >= 1 whose pr[i] is not >= thr
   int keep = k;
   if (P.min_p > 0.0f) {
     const double thr = readlane_f64(pr[0], 0) * static_cast<double>(P.min_p);
 #pragma unroll
-    for (int j = kEpiJ - 1; j >= 0; --j) {
+    for (int j = J - 1; j >= 0; --j) {
       const int i = j * 64 + lane;
       const uint64_t fail = __ballot(i >= 1 && i < k && !(pr[j] >= thr));
       if (fail) keep = j * 64 + __ffsll(static_cast<long long>(fail)) - 1;
@@ -461,8 +476,8 @@ __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsm
   f.flags = 0;
   bool ok = true;
   {
-    double S[kEpiJ];
-    prefix_f64(pr, k, S);
+    double S[J];
+    prefix_f64<J>(pr, k, S);
     f.sum = elem_at(S, k - 1);
     int kf = keep;
     if (P.top_p > 0.0f && P.top_p < 1.0f) {
@@ -482,9 +497,9 @@ __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsm
     f.keep = kf;
     f.tot = elem_at(S, kf - 1);
     const double r0 = u * f.tot;
-    double D[kEpiJ];
+    double D[J];
 #pragma unroll
-    for (int j = 0; j < kEpiJ; ++j) D[j] = r0 - S[j];
+    for (int j = 0; j < J; ++j) D[j] = r0 - S[j];
     const int i = first_where(D, kf, [](double x) { return x <= 0.0; });
     const double band = kCutDelta * f.tot;
     const double di = elem_at(D, i < kf ? i : kf - 1);
@@ -500,7 +515,7 @@ __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsm
   }
   Cuts c = f;
   if (!ok || a.info) {
-    const Cuts e = cuts_sequential(P, pr, k, keep, u, ws);
+    const Cuts e = cuts_sequential(P.top_p, spr, k, keep, u, ws);
     if (!ok) {
       c = e;
       c.flags |= VSMP_FLAG_SEQ_CUTS;
@@ -538,7 +553,7 @@ __device__ __forceinline__ void epilogue_wave(const KArgs& a, int row, const vsm
   if (a.cand_ids && a.cand_cap > 0) {
     const int m = min(c.keep, a.cand_cap);
 #pragma unroll
-    for (int j = 0; j < kEpiJ; ++j) {
+    for (int j = 0; j < J; ++j) {
       const int i = j * 64 + lane;
       if (i < m) {
         a.cand_ids[static_cast<size_t>(row) * a.cand_cap + i] = comp_idx(sorted[i]);
@@ -1014,7 +1029,16 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
   if (tid < 64) {
     double u = 0.0;
     if (tid == 0) u = draw_u(a, row, P);
-    epilogue_wave(a, row, P, sm_top, k, sm_int[6], sm_int[5], readlane_f64(u, 0), reinterpret_cast<double*>(sm_buf));
+    double* spr = reinterpret_cast<double*>(sm_buf) + kEpiWs;  // src/sampler.cpp:79-83
+    const float mx = comp_val(sm_top[0]);
+    for (int i = tid; i < k; i += 64) spr[i] = numer(comp_val(sm_top[i]), mx, P.temp);
+    wave_lds_sync();
+    if (k <= 64)
+      epilogue_wave<1>(a, row, P, sm_top, spr, k, sm_int[6], sm_int[5], readlane_f64(u, 0),
+                       reinterpret_cast<double*>(sm_buf));
+    else
+      epilogue_wave<kEpiJ>(a, row, P, sm_top, spr, k, sm_int[6], sm_int[5], readlane_f64(u, 0),
+                           reinterpret_cast<double*>(sm_buf));
   }
 }
 
@@ -1490,6 +1514,8 @@ struct __align__(16) RowShared {
   uint32_t bins[2][kRowBins];  // 16-byte aligned: read as uint4 by the bucket search
   uint64_t sorted[kKmax];
   uint64_t top[kKmax];
+  double top_pr[kKmax];   // numerators of top[], in collection order
+  double spr[kKmax];      // numerators in sorted order
   uint64_t wmax[kRowW];
   uint64_t r64[kRowW];
   int rank[kKmax];
@@ -1515,6 +1541,21 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
   x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
   return static_cast<uint32_t>(x);
+}
+
+// Maximum over the 64 lanes of a wave (DPP row shifts and broadcasts; lane 63 collects it).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  int x = static_cast<int>(v);
+#define VSMP_DPP_MAX(ctrl, rm) \
+  x = static_cast<int>(max(static_cast<uint32_t>(x), static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, ctrl, rm, 0xf, false))))
+  VSMP_DPP_MAX(0x111, 0xf);
+  VSMP_DPP_MAX(0x112, 0xf);
+  VSMP_DPP_MAX(0x114, 0xf);
+  VSMP_DPP_MAX(0x118, 0xf);
+  VSMP_DPP_MAX(0x142, 0xa);
+  VSMP_DPP_MAX(0x143, 0xc);
+#undef VSMP_DPP_MAX
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(x, 63));
 }
 
 // One wave searches 2048 bins from the top (bucket 2047 first) for the first bucket whose running
@@ -1596,7 +1637,7 @@ __device__ void wave_sort_buf(uint64_t* buf, int n) {
 
 // General rows in row mode: one pass for the row maximum / minimum (penalty in place) and the
 // penalty bitmap, which k_general then uses (as a single slice).
-__device__ void rows_general_prepass(const KArgs& a, int row, const vsmp_params& P, bool pen, const uint32_t* bits,
+__device__ __forceinline__ void rows_general_prepass(const KArgs& a, int row, const vsmp_params& P, bool pen, const uint32_t* bits,
                                      RowShared& sh) {
   const int tid = threadIdx.x;
   const int V = a.V;
@@ -1795,12 +1836,12 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   const int c0 = w;
   int cA = c0, cB = w + kRowW;
   row_load(rp4, V4, cA, lane, bA);
-  row_load(rp4, V4, cB, lane, bB);
   for (int i = tid; i < 2 * kRowBins; i += kRowNT) (&sh.bins[0][0])[i] = 0u;
   if (tid < kKmax) sh.rank[tid] = 0;
   if (tid == 0) {
     sh.ints[8] = 0;
     sh.ints[9] = 2 * kRowW;
+    sh.ints[10] = 0;
   }
 
   // -- penalty bitmap (src/sampler.cpp:53-65)
@@ -1831,22 +1872,43 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   uint4* park = reinterpret_cast<uint4*>(sh.wbuf[w]);  // kRowU * 64 groups = the wave's 4 KB
 #pragma unroll
   for (int u = 0; u < kRowU; ++u) park[u * 64 + lane] = bA[u];
+  // the first chunks arrive sooner when the second wave of requests waits for them
+  row_load(rp4, V4, cB, lane, bB);
   cA = grab_chunk(&sh.ints[9]);
   row_load(rp4, V4, cA, lane, bA);
   atomicAdd(&sh.bins[0][lm >> 21], 1u);
+  {
+    const uint32_t wl = wave_max_u32(lm);
+    if (lane == 0) atomicMax(reinterpret_cast<uint32_t*>(&sh.ints[10]), wl);
+  }
   __syncthreads();
   if (w == 0) wave_find_bucket(sh.bins[0], ks, sh.ints);
   __syncthreads();
   const int b1 = sh.ints[0];
   if (static_cast<int>(lm >> 21) == b1) atomicAdd(&sh.bins[1][(lm >> 10) & 2047u], 1u);
+  // bins[0] is read no more until the first pass of the final select, which each wave takes
+  // right after its stream: cleared here, before the barriers that precede every stream
+  for (int i = tid; i < kRowBins; i += kRowNT) sh.bins[0][i] = 0u;
   __syncthreads();
   if (w == 0) wave_find_bucket(sh.bins[1], ks - sh.ints[1], sh.ints + 4);
   __syncthreads();
   const int b2 = sh.ints[4];
   uint32_t T = (b1 >= 0 && b2 >= 0) ? ((static_cast<uint32_t>(b1) << 21) | (static_cast<uint32_t>(b2) << 10)) : 0u;
   T = __builtin_amdgcn_readfirstlane(T);
-  // both bin arrays start the final select cleared (ordered by the barrier after the stream)
-  for (int i = tid; i < 2 * kRowBins; i += kRowNT) (&sh.bins[0][0])[i] = 0u;
+  // bins[1] serves a second pass of the final select (ordered by the barrier after the stream)
+  for (int i = tid; i < kRowBins; i += kRowNT) sh.bins[1][i] = 0u;
+  // Window of the final select's first pass: [lo0, hi0] from T to the largest key of the first
+  // sixteen chunks, at most 2047 buckets wide; composites above hi0 share bucket 2047.
+  const uint64_t lo0 = static_cast<uint64_t>(T) << 32;
+  const uint64_t hi0 = (static_cast<uint64_t>(static_cast<uint32_t>(sh.ints[10])) << 32) | 0xFFFFFFFFull;
+  int s0 = 0;
+  {
+    const uint64_t R = hi0 - lo0;
+    if (R > 2046ull) {
+      s0 = 53 - __clzll(static_cast<long long>(R));
+      if ((R >> s0) > 2046ull) ++s0;
+    }
+  }
 
   // -- stream: append keys >= T (and > the wave's own bound tw once its buffer has compacted)
   uint64_t* buf = sh.wbuf[w];
@@ -1862,20 +1924,39 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     if (c0 < nch)
       row_process(pk, c0, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
   }
-  while (cB < nch) {  // cB < cA: a wave past the row on cB is past it on cA
-    const int nB = grab_chunk(&sh.ints[9]);
-    row_process(bB, cB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
-    row_load(rp4, V4, nB, lane, bB);
-    const int nA = grab_chunk(&sh.ints[9]);
-    if (cA < nch)
+  // Chunks go cB < cA < next cB < next cA ... The loop leaves as soon as a grab runs past the row,
+  // after processing what is still in flight, so no load is ever issued past the row here (the
+  // tail would otherwise first wait for such loads, queued behind the other waves' misses).
+  if (cB < nch) {
+    for (;;) {
+      const int nB = grab_chunk(&sh.ints[9]);
+      row_process(bB, cB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
+      if (nB >= nch) {
+        if (cA < nch)
+          row_process(bA, cA, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix,
+                      lt_mask);
+        break;
+      }
+      row_load(rp4, V4, nB, lane, bB);
+      const int nA = grab_chunk(&sh.ints[9]);
       row_process(bA, cA, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
-    row_load(rp4, V4, nA, lane, bA);
-    cB = nB;
-    cA = nA;
+      if (nA >= nch) {
+        row_process(bB, nB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix,
+                    lt_mask);
+        break;
+      }
+      row_load(rp4, V4, nA, lane, bA);
+      cB = nB;
+      cA = nA;
+    }
   }
   if (fix) fix_history(buf, fixed, cnt, bits, P.repeat);
   uint64_t wmx = 0ull;
-  for (int i = lane; i < cnt; i += 64) wmx = max64(wmx, buf[i]);
+  for (int i = lane; i < cnt; i += 64) {
+    const uint64_t c = buf[i];
+    wmx = max64(wmx, c);
+    if (path != kPathGreedy && c >= lo0) atomicAdd(&sh.bins[0][c > hi0 ? 2047 : (c - lo0) >> s0], 1u);
+  }
   for (int o = 32; o > 0; o >>= 1) wmx = max64(wmx, __shfl_xor(wmx, o));
   uint32_t np = 0;
   if (a.info && pen) {
@@ -1911,17 +1992,32 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     return;
   }
 
-  // -- exact ks-th largest composite: radix select over a shrinking window [lo, hi] of composites,
-  // 2048 buckets per pass; it ends as soon as the bucket holding the ks-th is taken whole (usually
-  // after the first pass). Penalised entries below T cannot be in the top ks and stay outside.
-  uint64_t lo = static_cast<uint64_t>(T) << 32, hi = maxc;
+  // -- exact ks-th largest composite. The first pass's histogram was taken by each wave just now;
+  // further passes (rare) narrow a window [lo, hi] by 2048 buckets each. It ends as soon as the
+  // bucket holding the ks-th is taken whole. Penalised entries below T cannot be in the top ks.
+  if (w == 0) wave_find_bucket(sh.bins[0], ks, sh.ints);
+  __syncthreads();
+  uint64_t lo, hi;
   int need = ks;
-  for (int pass = 0; pass < 8; ++pass) {
+  {
+    const int b = sh.ints[0];
+    need -= sh.ints[1];
+    const int inb = sh.ints[2];
+    if (b == 2047) {
+      lo = hi0 + 1;
+      hi = maxc;
+    } else {
+      lo = lo0 + (static_cast<uint64_t>(b < 0 ? 0 : b) << s0);
+      const uint64_t wdt = (1ull << s0) - 1ull;
+      hi = (hi0 - lo < wdt) ? hi0 : lo + wdt;
+    }
+    if (b < 0 || inb == need) hi = lo;  // done (b < 0 is unreachable: ks composites lie at or above lo0)
+  }
+  for (int pass = 1; lo != hi && pass < 9; ++pass) {
     const uint64_t R = hi - lo;
     const int sft = R < static_cast<uint64_t>(kRowBins) ? 0 : 53 - __clzll(static_cast<long long>(R));
     uint32_t* bins = sh.bins[pass & 1];
-    if (pass >= 1)
-      for (int i = tid; i < kRowBins; i += kRowNT) sh.bins[(pass + 1) & 1][i] = 0u;
+    for (int i = tid; i < kRowBins; i += kRowNT) sh.bins[(pass + 1) & 1][i] = 0u;
     for (int i = lane; i < cnt; i += 64) {
       const uint64_t c = buf[i];
       if (c >= lo && c <= hi) atomicAdd(&bins[(c - lo) >> sft], 1u);
@@ -1930,14 +2026,14 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     if (w == 0) wave_find_bucket(bins, need, sh.ints);
     __syncthreads();
     const int b = sh.ints[0];
-    if (b < 0) break;  // unreachable: at least ks composites lie at or above lo
+    if (b < 0) break;  // unreachable
     need -= sh.ints[1];
     const int inb = sh.ints[2];
     const uint64_t nlo = lo + (static_cast<uint64_t>(b) << sft);
     const uint64_t wdt = sft == 0 ? 0ull : (1ull << sft) - 1ull;
     hi = (hi - nlo < wdt) ? hi : nlo + wdt;
     lo = nlo;
-    if (inb == need) break;  // the whole bucket is taken: the top ks are the composites >= lo
+    if (inb == need) hi = lo;  // the whole bucket is taken: the top ks are the composites >= lo
   }
 
   // -- collect the composites >= lo (exactly ks of them)
@@ -1957,38 +2053,41 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   __syncthreads();
   const int nt = min(sh.ints[8], ks);
 
-  // -- sort them by rank (composites are distinct), then the reference epilogue on wave 0
-  if (nt > 64) {
-    const int parts = kRowNT / nt;  // >= 4
-    const int i = tid % nt, part = tid / nt;
-    if (part < parts) {
+  // -- ranks (composites are distinct): every thread counts the entries above one candidate in a
+  // share of the list; then wave 0 places them and runs the reference epilogue
+  {
+    const int i = tid & 63;
+    const int parts = nt <= 64 ? kRowW : kRowNT / nt;
+    const int part = nt <= 64 ? w : tid / nt;
+    const int ci = nt <= 64 ? i : tid % nt;
+    if (part < parts && ci < nt) {
       const int chunk = (nt + parts - 1) / parts;
-      const uint64_t x = sh.top[i];
+      const uint64_t x = sh.top[ci];
       int r = 0;
       const int j1 = min(nt, (part + 1) * chunk);
       for (int j = part * chunk; j < j1; ++j) r += sh.top[j] > x;
-      if (r) atomicAdd(&sh.rank[i], r);
+      if (r) atomicAdd(&sh.rank[ci], r);
     }
-    __syncthreads();
+    // wave 0 also takes the numerators (src/sampler.cpp:79-83), in collection order
+    if (w == 0) {
+      const float mx = comp_val(maxc);
+      for (int j = lane; j < nt; j += 64) sh.top_pr[j] = numer(comp_val(sh.top[j]), mx, P.temp);
+    }
   }
+  __syncthreads();
   if (w == 0) {
-    if (nt <= 64) {
-      if (lane >= nt) sh.top[lane] = 0ull;  // zero ranks below every composite
-      wave_lds_sync();
-      const uint64_t x = sh.top[lane];
-      const ulonglong2* t2 = reinterpret_cast<const ulonglong2*>(sh.top);
-      int r = 0;
-#pragma unroll
-      for (int j = 0; j < 32; ++j) {
-        const ulonglong2 y = t2[j];
-        r += (y.x > x) + (y.y > x);
-      }
-      if (lane < nt) sh.sorted[r] = x;
-    } else {
-      for (int i = lane; i < nt; i += 64) sh.sorted[sh.rank[i]] = sh.top[i];
+    for (int i = lane; i < nt; i += 64) {
+      const int r = sh.rank[i];
+      sh.sorted[r] = sh.top[i];
+      sh.spr[r] = sh.top_pr[i];
     }
     wave_lds_sync();
-    epilogue_wave(a, row, P, sh.sorted, nt, n_pen, 0, readlane_f64(u0, 0), reinterpret_cast<double*>(&sh.wbuf[0][0]));
+    if (nt <= 64)
+      epilogue_wave<1>(a, row, P, sh.sorted, sh.spr, nt, n_pen, 0, readlane_f64(u0, 0),
+                       reinterpret_cast<double*>(&sh.wbuf[0][0]));
+    else
+      epilogue_wave<kEpiJ>(a, row, P, sh.sorted, sh.spr, nt, n_pen, 0, readlane_f64(u0, 0),
+                           reinterpret_cast<double*>(&sh.wbuf[0][0]));
   }
 }
 
