@@ -118,6 +118,11 @@ VSMP_API int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, l
 VSMP_API int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params* params,
                             const int* hist, int H, double u, int* out_id, vsmp_row_info* info);
 
+/* Diagnostics, no reference counterpart: streams `bytes` (a multiple of 16; p 16-byte aligned)
+ * from device memory through a plain grid-stride read kernel on `stream`. bytes / its duration is
+ * the attainable HBM read bandwidth that the sampler's roofline is compared with. Returns 0 or -1. */
+VSMP_API int vsmp_read_probe(vsmp_ctx* ctx, const void* p, long long bytes, void* stream);
+
 /* A drop-in sampler object: verbo::Sampler (reference include/verbo/verbo.hpp:116-132) behind
  * a C handle, for FFI callers. Its history, xorshift stream and seeding are the reference's
  * (src/sampler.cpp:24-48); pick runs on the GPU through the calling thread's context. */

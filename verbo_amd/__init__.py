@@ -119,6 +119,7 @@ def load_library():
         "vsmp_sampler_pick": (ctypes.c_int, [_P, _P, ctypes.c_int]),
         "vsmp_sampler_accept": (None, [_P, ctypes.c_int]),
         "vsmp_sampler_reset": (None, [_P]),
+        "vsmp_read_probe": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -230,6 +231,16 @@ class Context:
         if rc != 0:
             raise _err()
         return out
+
+    def read_probe(self, t, stream=None):
+        """vsmp_read_probe: stream the bytes of device tensor `t` through a plain read kernel on
+        `stream` (default: torch's current stream). For measuring attainable read bandwidth."""
+        import torch
+
+        st = stream if stream is not None else torch.cuda.current_stream(t.device)
+        nbytes = t.numel() * t.element_size() // 16 * 16
+        if _lib.vsmp_read_probe(self._h, t.data_ptr(), nbytes, ctypes.c_void_p(st.cuda_stream)) != 0:
+            raise _err()
 
     def pick_host(self, logits, params, hist=(), u=0.0, with_info=False):
         """vsmp_pick_host: one pick on a host row (numpy). Returns id (and RowInfo)."""

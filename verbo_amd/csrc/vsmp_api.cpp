@@ -344,4 +344,16 @@ int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params*
   return 0;
 }
 
+int vsmp_read_probe(vsmp_ctx* ctx, const void* p, long long bytes, void* stream) {
+  vsmp::clear_error();
+  if (!ctx || !p) return vsmp::set_error("vsmp: null argument");
+  if (bytes <= 0 || bytes % 16 != 0 || reinterpret_cast<uintptr_t>(p) % 16 != 0)
+    return vsmp::set_error("vsmp: read probe needs a positive multiple of 16 bytes at a 16-byte aligned address");
+  if (!vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  if (!vsmp::grow(ctx->s_cnt, ctx->n_cnt, 8, false, "read probe sink")) return -1;
+  hipStream_t st = static_cast<hipStream_t>(stream);  // NULL: the default stream, as for vsmp_pick_batch
+  vsmp::launch_read_probe(p, bytes / 16, reinterpret_cast<unsigned*>(ctx->s_cnt), 16 * ctx->cus, st);
+  return vsmp::hip_ok(hipGetLastError(), "read-probe launch") ? 0 : -1;
+}
+
 }  // extern "C"
