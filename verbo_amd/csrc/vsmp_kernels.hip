@@ -5,16 +5,20 @@
 // ~index. Larger composite = earlier in the reference's sort order (value desc, index asc,
 // src/sampler.cpp:71), so every selection below is exact and independent of summation order.
 //
-// Three kernels, stream-ordered (each kernel boundary publishes the previous one's results; no
+// Kernels, stream-ordered (each kernel boundary publishes the previous one's results; no
 // workgroup waits on another):
-//  k_stage1  grid = rows x slices. Each workgroup loads one slice of one row into registers (the
-//            single HBM pass), applies the repetition penalty from an LDS bitmap of the row's
-//            history window, and writes its slice maximum; small-k rows (k <= 256) also write the
-//            slice's exact, sorted top-k.
+//  k_rows    one 1024-thread workgroup per row, for batches with at least one row per CU: streams
+//            the row once (penalty from an LDS bitmap of the history window), keeps only elements
+//            above a row bound taken from its first chunks, selects the exact top-k and runs the
+//            reference's epilogue (softmax numerators, min-p, top-p, draw).
+//  k_stage1  smaller batches, grid = rows x slices. Each workgroup loads one slice of one row into
+//            registers (the single HBM pass), applies the penalty and writes its slice maximum;
+//            small-k rows (k <= 256) also write the slice's exact, sorted top-k.
 //  k_finish  one workgroup per greedy / small-k row: merges the slice results and runs the
-//            reference's sequential fp64 epilogue (softmax numerators, min-p, top-p, draw).
+//            epilogue.
 //  k_general one workgroup per remaining row (k > 256 or top-k off): multi-pass radix select by
 //            count and by fp64 mass over the row, with histograms in LDS.
+//  k_read_probe  a plain streaming read, for the attainable-bandwidth measurement.
 #include <cfloat>
 
 #include "vsmp_common.hpp"
