@@ -211,13 +211,35 @@ __device__ void bitonic_desc(uint64_t* s, int n) {
 
 // Sorted top-`ks` of cnt distinct composites in buf -> top[0..ks). Rank counting for short lists,
 // bitonic sort for longer ones (buf is clobbered).
+// Entries of buf[0, n) greater than x. buf must be 16-byte aligned and hold zeros (which rank
+// below every composite) from n up to the next multiple of 16: sixteen entries per step, read as
+// eight 16-byte loads issued together.
+__device__ __forceinline__ int rank_count(const uint64_t* buf, int n, uint64_t x) {
+  const ulonglong2* b2 = reinterpret_cast<const ulonglong2*>(buf);
+  int r = 0;
+  for (int j = 0; j < n; j += 16) {
+    ulonglong2 y[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) y[t] = b2[(j >> 1) + t];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) r += static_cast<int>(y[t].x > x) + static_cast<int>(y[t].y > x);
+  }
+  return r;
+}
+
+// Zero-pads buf[n, roundup(n, 16)) for rank_count (block-wide; the caller synchronises).
+__device__ __forceinline__ void pad16(uint64_t* buf, int n, int tid) {
+  if (tid < ((n + 15) & ~15) - n) buf[n + tid] = 0ull;
+}
+
 template <int NT>
 __device__ void select_top(uint64_t* buf, int cnt, int ks, uint64_t* top) {
   if (cnt <= 2 * NT) {
+    pad16(buf, cnt, threadIdx.x);
+    __syncthreads();
     for (int i = threadIdx.x; i < cnt; i += NT) {
       const uint64_t x = buf[i];
-      int r = 0;
-      for (int j = 0; j < cnt; ++j) r += buf[j] > x;
+      const int r = rank_count(buf, cnt, x);
       if (r < ks) top[r] = x;
     }
     __syncthreads();
@@ -701,7 +723,7 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
   constexpr int WORDS = EPT * kTpb / 32;
   __shared__ uint32_t sm_bits[WORDS];
   __shared__ uint32_t sm_wl[kTpb];  // 4 wave-sorted lists of per-thread maxima
-  __shared__ uint64_t sm_buf[kCandCap];
+  __shared__ __align__(16) uint64_t sm_buf[kCandCap];
   __shared__ uint64_t sm_pen[kPenCap];
   __shared__ uint64_t sm_top[kKmax];
   __shared__ uint64_t sm_red64[kTpb / 64];
@@ -1000,32 +1022,46 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
   }
   __syncthreads();
   const int M = sm_off[S];
-  if (M <= 2 * kTpb) {
-    // one pass: rank of every entry among all (composites are distinct)
-    for (int i = tid; i < M; i += kTpb) {
-      int s = 0;
-      while (sm_off[s + 1] <= i) ++s;
-      sm_buf[i] = a.s_cand[static_cast<size_t>(row * S + s) * kKmax + (i - sm_off[s])];
+  // Each slice list is sorted, so with m = ceil(k / S) the smallest m-th entry over the lists that
+  // hold m bounds the row's k-th composite from below whenever those lists hold k entries in all:
+  // only entries at or above it can be in the top k.
+  uint64_t lb = 0ull;
+  {
+    const int m = (k + S - 1) / S;
+    int full = 0;
+    uint64_t mn = ~0ull;
+    for (int s2 = 0; s2 < S; ++s2) {
+      const int len = sm_off[s2 + 1] - sm_off[s2];
+      if (len >= m) {
+        ++full;
+        mn = min64(mn, a.s_cand[static_cast<size_t>(row * S + s2) * kKmax + (m - 1)]);
+      }
     }
+    if (static_cast<long long>(full) * m >= k) lb = mn;
+  }
+  if (tid == 0) sm_int[7] = 0;
+  __syncthreads();
+  for (int i = tid; i < M; i += kTpb) {
+    int s2 = 0;
+    while (sm_off[s2 + 1] <= i) ++s2;
+    const uint64_t v = a.s_cand[static_cast<size_t>(row * S + s2) * kKmax + (i - sm_off[s2])];
+    if (v >= lb) sm_buf[atomicAdd(&sm_int[7], 1)] = v;
+  }
+  __syncthreads();
+  const int C = sm_int[7];  // >= k
+  if (C <= 2 * kTpb) {
+    // rank by counting (composites are distinct)
+    pad16(sm_buf, C, tid);
     __syncthreads();
-    for (int i = tid; i < M; i += kTpb) {
+    for (int i = tid; i < C; i += kTpb) {
       const uint64_t x = sm_buf[i];
-      int r = 0;
-      for (int j = 0; j < M; ++j) r += sm_buf[j] > x;
+      const int r = rank_count(sm_buf, C, x);
       if (r < k) sm_top[r] = x;
     }
   } else {
     int p2 = 1;
-    while (p2 < M) p2 <<= 1;
-    for (int i = tid; i < p2; i += kTpb) {
-      uint64_t v = 0ull;
-      if (i < M) {
-        int s = 0;
-        while (sm_off[s + 1] <= i) ++s;
-        v = a.s_cand[static_cast<size_t>(row * S + s) * kKmax + (i - sm_off[s])];
-      }
-      sm_buf[i] = v;
-    }
+    while (p2 < C) p2 <<= 1;
+    for (int i = C + tid; i < p2; i += kTpb) sm_buf[i] = 0ull;
     bitonic_desc<kTpb>(sm_buf, p2);
     for (int i = tid; i < k; i += kTpb) sm_top[i] = sm_buf[i];
   }
