@@ -3,9 +3,10 @@
 // the same data members in the same order (the reference header compiles Sampler::cfg() inline
 // into its callers, so the object layout is part of the interface).
 //
-// Inside the reference build the drop-in sources (verbo_amd/csrc/sampler.cpp, generate.cpp)
-// compile against the reference's own header; this header lets them, and the generate() test
-// double, compile on their own. Config is reduced to the one field the sampler path reads.
+// libvsmp.so exports verbo::Sampler and verbo::generate built against this header, and a verbo
+// build links them in place of its src/sampler.cpp, so every type they touch keeps the
+// reference's exact layout: Config (generate reads cfg().vocab), Sampling, Stats, GenOpts, and the
+// single pointer members of Model, Session, Tokenizer and Detok.
 #pragma once
 
 #include <cstddef>
@@ -20,12 +21,38 @@ namespace verbo {
 
 enum class DType : std::uint8_t { F32 = 0, Q8 = 1, Q4 = 2 };
 
-// Model configuration; the sampler path reads only `vocab` (reference src/sampler.cpp:115).
+// Model configuration (reference include/verbo/verbo.hpp:18-36); the sampler path reads `vocab`.
 struct Config {
+  std::string arch;
+  int dim = 0;
+  int hidden = 0;
+  int layers = 0;
+  int heads = 0;
+  int kv_heads = 0;
+  int head_dim = 0;
   int vocab = 0;
+  int max_ctx = 0;
+  float eps = 1e-5f;
+  float theta = 10000.0f;
+  bool qkv_bias = false;
+  bool tied = false;
+  float rope_factor = 0.0f;
+  float rope_low = 1.0f;
+  float rope_high = 4.0f;
+  int rope_orig = 8192;
 };
 
-class Tokenizer;
+// The tokenizer (reference include/verbo/verbo.hpp:38-54); generate reaches it through Detok.
+class Tokenizer {
+ public:
+  std::string piece(int id) const;
+  int size() const;
+
+  struct Impl;
+
+ private:
+  std::shared_ptr<const Impl> impl_;
+};
 
 // Sampling parameters and their defaults (reference include/verbo/verbo.hpp:56-64).
 struct Sampling {

@@ -4,6 +4,8 @@ import ctypes
 import re
 from pathlib import Path
 
+import pytest
+
 import verbo_amd as V
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -49,3 +51,18 @@ def test_drop_in_header_keeps_sampler_layout():
     for line in ["float temp = 0.7f;", "int top_k = 40;", "float top_p = 0.9f;", "float min_p = 0.0f;",
                  "float repeat = 1.0f;", "int repeat_last = 64;", "std::uint64_t seed = 0;"]:
         assert line in h
+
+
+@pytest.mark.skipif(not Path("/root/reference/include/verbo/verbo.hpp").is_file(), reason="reference tree absent")
+def test_drop_in_types_have_the_reference_layout(tmp_path):
+    """Every type the drop-in Sampler and generate share with verbo has the reference header's
+    size and field offsets (tests/generate/layout.cpp built against both headers)."""
+    import subprocess
+
+    outs = []
+    for inc in (ROOT / "include", Path("/root/reference/include")):
+        exe = tmp_path / f"layout_{len(outs)}"
+        subprocess.run(["g++", "-std=c++17", "-I", str(inc), "-o", str(exe), str(ROOT / "tests" / "generate" / "layout.cpp")],
+                       check=True)
+        outs.append(subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout)
+    assert outs[0] == outs[1], outs

@@ -2,7 +2,9 @@
 
     python -m verbo_amd.build        # or verbo_amd.build.build()
 
-The library holds the HIP kernels, the C ABI (include/vsmp.h) and the drop-in verbo::Sampler.
+The library holds the HIP kernels, the C ABI (include/vsmp.h) and the drop-in verbo::Sampler. The
+drop-in verbo::generate (csrc/generate.cpp, plain C++) calls verbo's Session and Model, so it is
+compiled with the program that provides them: verbo's own build, or the test double.
 """
 import os
 import shutil
