@@ -16,7 +16,7 @@ constexpr int kMergeCap = 4096;  // per-row LDS capacity of the last-slice merge
 constexpr int kMaxMergeSlices = 64;  // slices a small-k row may be cut into
 constexpr int kGenThreads = 1024;  // threads per general-path workgroup (one row each)
 constexpr int kGenBuckets = 4096;  // level-0 mass buckets of the general path
-constexpr int kGenCap = 2048;      // elements the general path sorts in LDS at once
+constexpr int kGenCap = 1024;      // elements the general path sorts in LDS at once (power of two)
 constexpr int kMaxVocab = 1 << 26;
 constexpr int kRowMaxVocab = 1 << 19;                    // row mode keeps the row's bitmap in LDS
 constexpr size_t kRowMaxDynLds = (kRowMaxVocab / 32) * 4;

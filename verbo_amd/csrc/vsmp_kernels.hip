@@ -1105,21 +1105,27 @@ __device__ __forceinline__ float4 load4(const float* rp, int e, int V) {
   return v;
 }
 
-// Calls f(composite, value) for every element of the row, penalty applied.
+// Calls f(composite, value) for every element of the row, penalty applied. Two iterations of
+// loads in flight (a and b); every load is issued unconditionally (past the row it rereads the last
+// 16-byte group, which 4*ceil(V/4) <= ld keeps inside the row), so each wait covers exactly the
+// buffer about to be processed.
 template <class F>
 __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
-  constexpr int U = 2;
+  constexpr int U = 1;
   constexpr int step = kGenThreads * 4 * U;
-  for (int base = 0; base < R.V; base += step) {
-    float4 v[U];
+  const int tid = static_cast<int>(threadIdx.x);
+  const float4* rp4 = reinterpret_cast<const float4*>(R.rp);
+  const int V4 = (R.V + 3) >> 2;
+  const int nit = (R.V + step - 1) / step;
+  float4 a[U], b[U];
+  auto load = [&](int it, float4 (&v)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = rp4[min(it * (step / 4) + u * kGenThreads + tid, V4 - 1)];
+  };
+  auto process = [&](int it, const float4 (&v)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int e = base + (u * kGenThreads + static_cast<int>(threadIdx.x)) * 4;
-      if (e < R.V) v[u] = load4(R.rp, e, R.V);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int e = base + (u * kGenThreads + static_cast<int>(threadIdx.x)) * 4;
+      const int e = it * step + (u * kGenThreads + tid) * 4;
       if (e >= R.V) continue;
       const uint32_t nib = R.pen ? (R.bits[e >> 5] >> (e & 31)) & 0xFu : 0u;
       const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
@@ -1132,16 +1138,30 @@ __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
         }
       }
     }
+  };
+  load(0, a);
+  load(1, b);
+  for (int it = 0; it < nit; it += 2) {
+    process(it, a);
+    load(it + 2, a);
+    if (it + 1 < nit) process(it + 1, b);
+    load(it + 3, b);
   }
 }
 
 struct GenShared {
   uint32_t cnt0[kGenBuckets];   // level-0 inclusive prefix counts (by mass bucket q)
   double mass0[kGenBuckets];    // level-0 inclusive prefix masses
-  uint32_t rcnt[kRefBuckets];   // refinement histogram
-  double rmass[kRefBuckets];
-  uint64_t list[kGenCap];       // collected composites
-  double lpr[kGenCap];          // their weights / prefix sums
+  union {                       // a refinement's histograms, then the elements it collects
+    struct {
+      uint32_t rcnt[kRefBuckets];
+      double rmass[kRefBuckets];
+    };
+    struct {
+      uint64_t list[kGenCap];   // collected composites
+      double lpr[kGenCap];      // their weights / prefix sums
+    };
+  };
   double wm[kGenNW];
   uint32_t wc[kGenNW];
   uint64_t r64[kGenNW];
@@ -1165,9 +1185,18 @@ struct GenCtx {
   GenRow R;
   float mx;
   float temp;
+  double inv_temp;
   float qs;      // level-0 bucket scale
   uint64_t ckk;  // top-k restriction: element in the prefix iff composite >= ckk
 };
+
+// The general path's numerator, exp(double(float(v - mx)) * (1 / temp)): the reference divides by
+// temp (src/sampler.cpp:83); the product differs by at most an ulp of the exponent argument, far
+// inside the tolerance this path is held to (its cuts are taken on fp64 sums in bucket order and
+// compared with the reference's margins). One function for every sum the path takes.
+__device__ __forceinline__ double numer_g(const GenCtx& g, float v) {
+  return exp(static_cast<double>(v - g.mx) * g.inv_temp);
+}
 
 __device__ __forceinline__ int q_of(const GenCtx& g, float v) {
   const float t = (g.mx - v) * g.qs;
@@ -1180,7 +1209,7 @@ __device__ __forceinline__ int q_of(const GenCtx& g, float v) {
 // numerators (mass). Refines the composite range with 2048-bucket histograms until at most
 // kGenCap elements remain, then sorts those in LDS and scans them.
 template <bool MASS, class P>
-__device__ Sel refine_select(const GenCtx& g, GenShared& sh, P&& pred, uint64_t clo, uint64_t chi, int n,
+__device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, P&& pred, uint64_t clo, uint64_t chi, int n,
                              int rank_above, double above, double target) {
   const int tid = threadIdx.x;
   for (int level = 0; level < 8 && n > kGenCap && clo < chi; ++level) {
@@ -1196,7 +1225,7 @@ __device__ Sel refine_select(const GenCtx& g, GenShared& sh, P&& pred, uint64_t 
       if (ck < clo || ck > chi || !pred(ck, v)) return;
       const int d = static_cast<int>((ck - clo) >> shift);
       atomicAdd(&sh.rcnt[d], 1u);
-      if (MASS) atomicAdd(&sh.rmass[d], numer(v, g.mx, g.temp));
+      if (MASS) atomicAdd(&sh.rmass[d], numer_g(g, v));
     });
     __syncthreads();
     // scan buckets from the top (largest composites first): position p <-> bucket 2047 - p
@@ -1259,8 +1288,8 @@ __device__ Sel refine_select(const GenCtx& g, GenShared& sh, P&& pred, uint64_t 
   bitonic_desc<kGenThreads>(sh.list, p2);
   // two entries per thread, inclusive prefix of weights
   const int i0 = 2 * tid, i1 = i0 + 1;
-  const double w0 = i0 < m ? (MASS ? numer(comp_val(sh.list[i0]), g.mx, g.temp) : 1.0) : 0.0;
-  const double w1 = i1 < m ? (MASS ? numer(comp_val(sh.list[i1]), g.mx, g.temp) : 1.0) : 0.0;
+  const double w0 = i0 < m ? (MASS ? numer_g(g, comp_val(sh.list[i0])) : 1.0) : 0.0;
+  const double w1 = i1 < m ? (MASS ? numer_g(g, comp_val(sh.list[i1])) : 1.0) : 0.0;
   double em;
   uint32_t ec;
   block_excl_scan<kGenThreads>(w0 + w1, 0u, em, ec, sh.wm, sh.wc);
@@ -1322,6 +1351,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   g.R.bits = a.s_bits + static_cast<size_t>(row) * a.words;
   g.mx = comp_val(mxc);
   g.temp = P.temp;
+  g.inv_temp = 1.0 / static_cast<double>(P.temp);
   {
     float range = g.mx - key_val(static_cast<uint32_t>(mnk));
     const float cap = 64.0f * P.temp;
@@ -1360,7 +1390,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   uint64_t t_lastm = ~0ull, t_last = ~0ull;
   gen_pass(g.R, [&](uint64_t ck, float v) {
     if (ck < g.ckk) return;
-    const double p = numer(v, g.mx, g.temp);
+    const double p = numer_g(g, v);
     t_sum += p;
     t_last = min64(t_last, ck);
     if (minp && p >= thr) {
