@@ -1793,50 +1793,68 @@ __device__ __noinline__ WaveState row_compact(uint64_t* buf, WaveState st, int k
   return st;
 }
 
-// Appends the keys of one step that pass the filter (key >= T and key > tw) to the wave buffer.
+// The stream's filter, wave-uniform: a key passes when key > gt, i.e. key >= T and key > tw
+// (gt = max(T - 1, tw)). A value v < fl cannot pass (fl is the float whose key is gt + 1; NaN
+// when that is a NaN key, so that every element goes to the key test).
+struct RowFilter {
+  uint32_t gt;
+  float fl;
+};
+__device__ __forceinline__ RowFilter row_filter(uint32_t T, uint32_t tw) {
+  const uint32_t gt = T == 0u ? tw : max(T - 1u, tw);
+  const float fl = gt == 0xFFFFFFFFu ? __uint_as_float(0x7FC00000u) : key_val(gt + 1u);
+  return RowFilter{gt, fl};
+}
+
+// Appends the keys of one step that pass the filter to the wave buffer: one ballot per element
+// slot, positions by mbcnt; the count, the wave bound and the filter stay wave-uniform.
 __device__ __forceinline__ void row_append(const uint32_t (&kk)[4], int e0, uint32_t T, uint64_t* buf, int& cnt,
-                                           int& fixed, uint32_t& tw, int ks, bool fix, const uint32_t* bits, float rep,
-                                           uint64_t lt_mask) {
-  const uint32_t gm = max(max(kk[0], kk[1]), max(kk[2], kk[3]));
-  if (__any(gm >= T && gm > tw)) {
+                                           int& fixed, uint32_t& tw, RowFilter& rf, int ks, bool fix,
+                                           const uint32_t* bits, float rep) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      bool pred = kk[c] >= T && kk[c] > tw;
-      uint64_t m = __ballot(pred);
-      if (m) {
-        if (cnt + 64 > kWaveCap) {
-          const WaveState st = row_compact(buf, WaveState{cnt, fixed, tw}, ks, fix, bits, rep);
-          cnt = st.cnt;
-          fixed = st.fixed;
-          tw = st.tw;
-          pred = kk[c] >= T && kk[c] > tw;
-          m = __ballot(pred);
-        }
-        if (pred) buf[cnt + __popcll(m & lt_mask)] = comp(kk[c], static_cast<uint32_t>(e0 + c));
-        cnt += __popcll(m);
+  for (int c = 0; c < 4; ++c) {
+    uint64_t m = __ballot(kk[c] > rf.gt);
+    if (m) {
+      if (cnt + __popcll(m) > kWaveCap) {
+        const WaveState st = row_compact(buf, WaveState{cnt, fixed, tw}, ks, fix, bits, rep);
+        cnt = __builtin_amdgcn_readfirstlane(st.cnt);
+        fixed = __builtin_amdgcn_readfirstlane(st.fixed);
+        tw = __builtin_amdgcn_readfirstlane(st.tw);
+        rf = row_filter(T, tw);
+        m = __ballot(kk[c] > rf.gt);
       }
+      const int below = static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+      if (kk[c] > rf.gt) buf[cnt + below] = comp(kk[c], static_cast<uint32_t>(e0 + c));
+      cnt += __popcll(m);
     }
   }
 }
 
 __device__ __forceinline__ void row_process(const uint4 (&cv)[kRowU], int ch, int nfull, int lane, int V,
                                             bool inline_pen, bool pen, float rep, const uint32_t* bits, uint32_t T,
-                                            uint64_t* buf, int& cnt, int& fixed, uint32_t& tw, int ks, bool fix,
-                                            uint64_t lt_mask) {
+                                            uint64_t* buf, int& cnt, int& fixed, uint32_t& tw, RowFilter& rf, int ks,
+                                            bool fix) {
   const bool fast = __builtin_amdgcn_readfirstlane(static_cast<int>(ch < nfull && !inline_pen)) != 0;
 #pragma unroll
   for (int u = 0; u < kRowU; ++u) {
     uint32_t kk[4];
     if (fast) {
+      // one float compare per element; keys only for the steps where some element may pass
+      const float fl = rf.fl;
+      const uint64_t maybe = __ballot(!(__uint_as_float(cv[u].x) < fl)) | __ballot(!(__uint_as_float(cv[u].y) < fl)) |
+                             __ballot(!(__uint_as_float(cv[u].z) < fl)) | __ballot(!(__uint_as_float(cv[u].w) < fl));
+      if (maybe == 0ull) continue;
       kk[0] = key_of(cv[u].x);
       kk[1] = key_of(cv[u].y);
       kk[2] = key_of(cv[u].z);
       kk[3] = key_of(cv[u].w);
     } else {
       row_keys_checked(cv[u], ch, u, lane, V, inline_pen, pen, false, rep, bits, kk);
+      if (__ballot(max(max(kk[0], kk[1]), max(kk[2], kk[3])) > rf.gt) == 0ull) continue;
     }
     const int e0 = 4 * ((ch * kRowU + u) * 64 + lane);
-    row_append(kk, e0, T, buf, cnt, fixed, tw, ks, fix, bits, rep, lt_mask);
+    row_append(kk, e0, T, buf, cnt, fixed, tw, rf, ks, fix, bits, rep);
   }
 }
 
@@ -1985,14 +2003,14 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   uint32_t tw = 0u;  // 0: only valid keys
   int cnt = 0, fixed = 0;
   const bool fix = pen && !inline_pen;
-  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  RowFilter rf = row_filter(T, tw);
   {
     uint4 pk[kRowU];  // the parked chunk, read back whole before its appends reuse the buffer
 #pragma unroll
     for (int u = 0; u < kRowU; ++u) pk[u] = park[u * 64 + lane];
     wave_lds_sync();
     if (c0 < nch)
-      row_process(pk, c0, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
+      row_process(pk, c0, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, rf, ks, fix);
   }
   // Chunks go cB < cA < next cB < next cA ... The loop leaves as soon as a grab runs past the row,
   // after processing what is still in flight, so no load is ever issued past the row here (the
@@ -2000,19 +2018,19 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   if (cB < nch) {
     for (;;) {
       const int nB = grab_chunk(&sh.ints[9]);
-      row_process(bB, cB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
+      row_process(bB, cB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, rf, ks, fix);
       if (nB >= nch) {
         if (cA < nch)
-          row_process(bA, cA, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix,
-                      lt_mask);
+          row_process(bA, cA, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, rf, ks,
+                      fix);
         break;
       }
       row_load(rp4, V4, nB, lane, bB);
       const int nA = grab_chunk(&sh.ints[9]);
-      row_process(bA, cA, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix, lt_mask);
+      row_process(bA, cA, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, rf, ks, fix);
       if (nA >= nch) {
-        row_process(bB, nB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, ks, fix,
-                    lt_mask);
+        row_process(bB, nB, nfull, lane, V, inline_pen, pen, P.repeat, bits, T, buf, cnt, fixed, tw, rf, ks,
+                    fix);
         break;
       }
       row_load(rp4, V4, nA, lane, bA);
@@ -2116,7 +2134,8 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     if (lane == 0 && m) base = atomicAdd(&sh.ints[8], __popcll(m));
     base = __shfl(base, 0);
     if (t) {
-      const int p = base + __popcll(m & lt_mask);
+      const int p = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
       if (p < kKmax) sh.top[p] = c;
     }
   }
