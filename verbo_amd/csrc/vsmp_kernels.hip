@@ -1105,7 +1105,7 @@ struct GenRow {
   float rep;
 };
 
-// Calls f(composite, value) for every element of the row, penalty applied. Two iterations of
+// Calls f(index, value) for every element of the row, penalty applied. Two iterations of
 // loads in flight (a and b); every load is issued unconditionally (past the row it rereads the last
 // 16-byte group, which 4*ceil(V/4) <= ld keeps inside the row), so each wait covers exactly the
 // buffer about to be processed.
@@ -1134,7 +1134,7 @@ __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
         if (e + c < R.V) {
           float fv = x[c];
           if (nib & (1u << c)) fv = penalise(fv, R.rep);
-          f(comp(ord_key(fv), static_cast<uint32_t>(e + c)), fv);
+          f(e + c, fv);
         }
       }
     }
@@ -1149,7 +1149,7 @@ __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
   }
 }
 
-struct GenShared {
+struct __align__(16) GenShared {  // list is read as 16-byte vectors
   uint32_t cnt0[kGenBuckets];   // level-0 inclusive prefix counts (by mass bucket q)
   double mass0[kGenBuckets];    // level-0 inclusive prefix masses
   union {                       // a refinement's histograms, then the elements it collects
@@ -1203,14 +1203,24 @@ __device__ __forceinline__ int q_of(const GenCtx& g, float v) {
   return t < static_cast<float>(kGenBuckets) ? static_cast<int>(t) : kGenBuckets - 1;
 }
 
+// atomicMin(dst, i) for the lane of this wave whose claim holds with the smallest lane index (the
+// callers' positions grow with the lane index): one LDS atomic per wave instead of one per lane,
+// where thousands of lanes can claim.
+__device__ __forceinline__ void wave_claim_min(int* dst, bool claim, int i) {
+  const uint64_t m = __ballot(claim);
+  if (m != 0ull && static_cast<int>(threadIdx.x & 63) == __ffsll(static_cast<long long>(m)) - 1) atomicMin(dst, i);
+}
+
 // Finds, among the elements accepted by `pred` whose composite lies in [clo, chi] (there are n of
 // them, preceded by `rank_above` elements of total weight `above`), the first element in sorted
 // order at which the running weight reaches `target`. Weights are 1 (count) or the fp64
 // numerators (mass). Refines the composite range with 2048-bucket histograms until at most
 // kGenCap elements remain, then sorts those in LDS and scans them.
-template <bool MASS, class P>
-__device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, P&& pred, uint64_t clo, uint64_t chi, int n,
-                             int rank_above, double above, double target) {
+constexpr int kGenRankMax = 384;  // longest collected list ranked by counting (else bitonic)
+
+template <bool MASS, class PV, class PC>
+__device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, PV&& pred_v, PC&& pred_c, uint64_t clo,
+                                             uint64_t chi, int n, int rank_above, double above, double target) {
   const int tid = threadIdx.x;
   for (int level = 0; level < 8 && n > kGenCap && clo < chi; ++level) {
     const uint64_t span = chi - clo;
@@ -1221,8 +1231,12 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, P&&
       sh.rmass[i] = 0.0;
     }
     __syncthreads();
-    gen_pass(g.R, [&](uint64_t ck, float v) {
-      if (ck < clo || ck > chi || !pred(ck, v)) return;
+    const uint32_t klo = comp_key(clo), khi = comp_key(chi);
+    gen_pass(g.R, [&](int e, float v) {
+      const uint32_t kv = ord_key(v);
+      if (kv < klo || kv > khi || !pred_v(v)) return;
+      const uint64_t ck = comp(kv, static_cast<uint32_t>(e));
+      if (ck < clo || ck > chi || !pred_c(ck)) return;
       const int d = static_cast<int>((ck - clo) >> shift);
       atomicAdd(&sh.rcnt[d], 1u);
       if (MASS) atomicAdd(&sh.rmass[d], numer_g(g, v));
@@ -1241,8 +1255,8 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, P&&
     __syncthreads();
     // first non-empty position whose inclusive weight reaches the target
     const double i0 = above + em + m0, i1 = i0 + m1;
-    if (c0 && i0 >= target) atomicMin(&sh.ints[0], p0);
-    if (c1 && i1 >= target) atomicMin(&sh.ints[0], p0 + 1);
+    const bool k0 = c0 && i0 >= target, k1 = c1 && i1 >= target;
+    wave_claim_min(&sh.ints[0], k0 || k1, k0 ? p0 : p0 + 1);
     __syncthreads();
     int pos = sh.ints[0];
     if (pos == kRefBuckets) {
@@ -1275,17 +1289,38 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, P&&
   // collect, sort, scan
   if (tid == 0) sh.ints[4] = 0;
   __syncthreads();
-  gen_pass(g.R, [&](uint64_t ck, float v) {
-    if (ck < clo || ck > chi || !pred(ck, v)) return;
+  {
+  const uint32_t klo = comp_key(clo), khi = comp_key(chi);
+  gen_pass(g.R, [&](int e, float v) {
+    const uint32_t kv = ord_key(v);
+    if (kv < klo || kv > khi || !pred_v(v)) return;
+    const uint64_t ck = comp(kv, static_cast<uint32_t>(e));
+    if (ck < clo || ck > chi || !pred_c(ck)) return;
     const int p = atomicAdd(&sh.ints[4], 1);
     if (p < kGenCap) sh.list[p] = ck;
   });
+  }
   __syncthreads();
   const int m = min(sh.ints[4], kGenCap);
-  int p2 = 1;
-  while (p2 < m) p2 <<= 1;
-  for (int i = m + tid; i < p2; i += kGenThreads) sh.list[i] = 0ull;
-  bitonic_desc<kGenThreads>(sh.list, p2);
+  if (m <= kGenRankMax) {
+    // short lists: each entry's rank by counting (composites are distinct), through lpr's storage
+    const int mpad = (m + 15) & ~15;
+    for (int i = m + tid; i < mpad; i += kGenThreads) sh.list[i] = 0ull;
+    __syncthreads();
+    uint64_t* tmp = reinterpret_cast<uint64_t*>(sh.lpr);
+    for (int i = tid; i < m; i += kGenThreads) {
+      const uint64_t x = sh.list[i];
+      tmp[rank_count(sh.list, m, x)] = x;
+    }
+    __syncthreads();
+    for (int i = tid; i < m; i += kGenThreads) sh.list[i] = tmp[i];
+    __syncthreads();
+  } else {
+    int p2 = 1;
+    while (p2 < m) p2 <<= 1;
+    for (int i = m + tid; i < p2; i += kGenThreads) sh.list[i] = 0ull;
+    bitonic_desc<kGenThreads>(sh.list, p2);
+  }
   // two entries per thread, inclusive prefix of weights
   const int i0 = 2 * tid, i1 = i0 + 1;
   const double w0 = i0 < m ? (MASS ? numer_g(g, comp_val(sh.list[i0])) : 1.0) : 0.0;
@@ -1297,8 +1332,8 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, P&&
   if (i1 < kGenCap) sh.lpr[i1] = above + em + w0 + w1;
   if (tid == 0) sh.ints[5] = m;
   __syncthreads();
-  if (i0 < m && sh.lpr[i0] >= target) atomicMin(&sh.ints[5], i0);
-  if (i1 < m && sh.lpr[i1] >= target) atomicMin(&sh.ints[5], i1);
+  const bool k0 = i0 < m && sh.lpr[i0] >= target, k1 = i1 < m && sh.lpr[i1] >= target;
+  wave_claim_min(&sh.ints[5], k0 || k1, k0 ? i0 : i1);
   __syncthreads();
   Sel s;
   if (m == 0) {  // empty range (cannot happen for a bucket chosen by its count; kept defensive)
@@ -1371,8 +1406,9 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   // top-k prefix when 256 < k < V: the k-th element by count
   g.ckk = 0ull;
   if (k < V) {
-    auto all = [](uint64_t, float) { return true; };
-    const Sel s = refine_select<false>(g, sh, all, static_cast<uint64_t>(static_cast<uint32_t>(mnk)) << 32, mxc, V, 0,
+    auto all_v = [](float) { return true; };
+    auto all_c = [](uint64_t) { return true; };
+    const Sel s = refine_select<false>(g, sh, all_v, all_c, static_cast<uint64_t>(static_cast<uint32_t>(mnk)) << 32, mxc, V, 0,
                                        0.0, static_cast<double>(k));
     g.ckk = s.ck;
   }
@@ -1387,31 +1423,39 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   const double thr = static_cast<double>(P.min_p);  // pr of the maximum is exactly 1
   double t_sum = 0.0, t_totm = 0.0;
   uint32_t t_cntm = 0;
-  uint64_t t_lastm = ~0ull, t_last = ~0ull;
-  gen_pass(g.R, [&](uint64_t ck, float v) {
-    if (ck < g.ckk) return;
+  const bool cut_k = g.ckk != 0ull;
+  gen_pass(g.R, [&](int e, float v) {
+    if (cut_k && comp(ord_key(v), static_cast<uint32_t>(e)) < g.ckk) return;
     const double p = numer_g(g, v);
     t_sum += p;
-    t_last = min64(t_last, ck);
     if (minp && p >= thr) {
       ++t_cntm;
       t_totm += p;
-      t_lastm = min64(t_lastm, ck);
     }
     const int q = q_of(g, v);
     atomicAdd(&sh.cnt0[q], 1u);
     atomicAdd(&sh.mass0[q], p);
   });
   const double sum = block_sum_f64<kGenThreads>(t_sum, sh.rd);
-  const uint64_t last_all = block_min64<kGenThreads>(t_last, sh.r64);
   double totm = 0.0;
   uint32_t cntm = 0;
-  uint64_t lastm = ~0ull;
   if (minp) {
     totm = block_sum_f64<kGenThreads>(t_totm, sh.rd);
     cntm = block_sum_u32<kGenThreads>(t_cntm, sh.r32);
-    lastm = block_min64<kGenThreads>(t_lastm, sh.r64);
   }
+  // The kept set's smallest composite (its last element in the reference's order), taken by a pass
+  // of its own only when it is needed: a draw that falls past the kept set (rounding) or the
+  // diagnostics. by_minp: the set is the min-p prefix (numerator >= thr), else the top-k prefix.
+  auto kept_last = [&](bool by_minp) -> uint64_t {
+    uint64_t t = ~0ull;
+    gen_pass(g.R, [&](int e, float v) {
+      const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
+      if (ck < g.ckk) return;
+      if (by_minp && !(numer_g(g, v) >= thr)) return;
+      t = min64(t, ck);
+    });
+    return block_min64<kGenThreads>(t, sh.r64);
+  };
   // level-0 inclusive prefixes (4 buckets per thread, bucket 0 = closest to the maximum)
   {
     const int b0 = 4 * tid;
@@ -1440,16 +1484,18 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   // src/sampler.cpp:86-91 (min-p), with the count of a prefix
   int keep = k;
   double tot = sum;
-  uint64_t last = last_all;
+  uint64_t last = 0ull;
+  int last_from = 0;  // 0: the top-k prefix's last, 1: the min-p prefix's last (both still to take), 2: `last`
   if (minp) {
     if (cntm >= 1u) {
       keep = static_cast<int>(cntm);
       tot = totm;
-      last = lastm;
+      last_from = 1;
     } else {
       keep = 1;
       tot = 1.0;
       last = mxc;
+      last_from = 2;
     }
   }
   const int keep_minp = keep;
@@ -1469,7 +1515,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     __syncthreads();
     for (int b = tid; b < kGenBuckets; b += kGenThreads) {
       const uint32_t prev = b > 0 ? sh.cnt0[b - 1] : 0u;
-      if (sh.cnt0[b] > prev && sh.mass0[b] >= target) atomicMin(&sh.ints[6], b);
+      wave_claim_min(&sh.ints[6], sh.cnt0[b] > prev && sh.mass0[b] >= target, b);
     }
     __syncthreads();
     const int qb = sh.ints[6];
@@ -1485,12 +1531,15 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     const int rank_above = qb > 0 ? static_cast<int>(sh.cnt0[qb - 1]) : 0;
     const int n = static_cast<int>(sh.cnt0[qb]) - rank_above;
     const uint64_t ckk = g.ckk;
-    auto in_q = [&g, ckk, qb](uint64_t ck, float v) { return ck >= ckk && q_of(g, v) == qb; };
+    auto in_q_v = [&g, qb](float v) { return q_of(g, v) == qb; };
+    auto in_q_c = [ckk](uint64_t ck) { return ck >= ckk; };
     uint64_t clo = 0ull, chi = ~0ull;
     if (n > kGenCap) {  // tighten the composite range to the bucket's
       uint64_t lo_ = ~0ull, hi_ = 0ull;
-      gen_pass(g.R, [&](uint64_t ck, float v) {
-        if (!in_q(ck, v)) return;
+      gen_pass(g.R, [&](int e, float v) {
+        if (!in_q_v(v)) return;
+        const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
+        if (!in_q_c(ck)) return;
         lo_ = min64(lo_, ck);
         hi_ = max64(hi_, ck);
       });
@@ -1498,7 +1547,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       chi = block_max64<kGenThreads>(hi_, sh.r64);
     }
     __syncthreads();
-    s = refine_select<true>(g, sh, in_q, clo, chi, n, rank_above, above, target);
+    s = refine_select<true>(g, sh, in_q_v, in_q_c, clo, chi, n, rank_above, above, target);
     return s;
   };
 
@@ -1512,6 +1561,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       keep = s.rank + 1;
       tot = s.incl;
       last = s.ck;
+      last_from = 2;
     }
   }
 
@@ -1522,6 +1572,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   u = sh.dbls[1];
   const double target = u * tot;
   const Sel d = mass_select(target);
+  if (last_from != 2 && (!(d.found && d.rank < keep) || a.info)) last = kept_last(last_from == 1);
   int id, rank;
   double margin;
   if (d.found && d.rank < keep) {
