@@ -1218,6 +1218,72 @@ __device__ __forceinline__ void wave_claim_min(int* dst, bool claim, int i) {
 // kGenCap elements remain, then sorts those in LDS and scans them.
 constexpr int kGenRankMax = 384;  // longest collected list ranked by counting (else bitonic)
 
+// Sorts list[0, m) descending (block-wide; the composites are distinct). Short lists: each entry's
+// rank by counting, placed through tmp (m entries); longer ones: bitonic, with list zero-padded to a
+// power of two (the caller's list has room).
+__device__ __forceinline__ void sort_desc(GenShared& sh, uint64_t* list, uint64_t* tmp, int m) {
+  const int tid = threadIdx.x;
+  if (m <= kGenRankMax) {
+    const int mpad = (m + 15) & ~15;
+    for (int i = m + tid; i < mpad; i += kGenThreads) list[i] = 0ull;
+    __syncthreads();
+    for (int i = tid; i < m; i += kGenThreads) {
+      const uint64_t x = list[i];
+      tmp[rank_count(list, m, x)] = x;
+    }
+    __syncthreads();
+    for (int i = tid; i < m; i += kGenThreads) list[i] = tmp[i];
+    __syncthreads();
+  } else {
+    int p2 = 1;
+    while (p2 < m) p2 <<= 1;
+    for (int i = m + tid; i < p2; i += kGenThreads) list[i] = 0ull;
+    bitonic_desc<kGenThreads>(list, p2);
+  }
+}
+
+// The first entry of the descending list[0, m) at which the running weight, starting from `above`
+// after `rank_above` elements, reaches target. Weights are 1 (count) or the fp64 numerators (mass);
+// lpr[0, m) receives the inclusive running weights. When rounding leaves the target just past the
+// list, its last entry (found = false).
+template <bool MASS>
+__device__ __forceinline__ Sel scan_sorted(const GenCtx& g, GenShared& sh, const uint64_t* list, double* lpr, int m,
+                                           int rank_above, double above, double target) {
+  const int tid = threadIdx.x;
+  const int i0 = 2 * tid, i1 = i0 + 1;
+  const double w0 = i0 < m ? (MASS ? numer_g(g, comp_val(list[i0])) : 1.0) : 0.0;
+  const double w1 = i1 < m ? (MASS ? numer_g(g, comp_val(list[i1])) : 1.0) : 0.0;
+  double em;
+  uint32_t ec;
+  block_excl_scan<kGenThreads>(w0 + w1, 0u, em, ec, sh.wm, sh.wc);
+  if (i0 < m) lpr[i0] = above + em + w0;
+  if (i1 < m) lpr[i1] = above + em + w0 + w1;
+  if (tid == 0) sh.ints[5] = m;
+  __syncthreads();
+  const bool k0 = i0 < m && lpr[i0] >= target, k1 = i1 < m && lpr[i1] >= target;
+  wave_claim_min(&sh.ints[5], k0 || k1, k0 ? i0 : i1);
+  __syncthreads();
+  Sel s;
+  if (m == 0) {  // empty range (cannot happen for a bucket chosen by its count; kept defensive)
+    s.found = false;
+    s.ck = 0ull;
+    s.rank = rank_above;
+    s.before = s.incl = above;
+    __syncthreads();
+    return s;
+  }
+  int j = sh.ints[5];
+  s.found = j < m;
+  if (!s.found) j = m - 1;  // rounding left the target just past this range: its last element
+  s.ck = list[j];
+  s.rank = rank_above + j;
+  s.before = j > 0 ? lpr[j - 1] : above;
+  s.incl = lpr[j];
+  __syncthreads();
+  return s;
+}
+
+
 template <bool MASS, class PV, class PC>
 __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, PV&& pred_v, PC&& pred_c, uint64_t clo,
                                              uint64_t chi, int n, int rank_above, double above, double target) {
@@ -1302,57 +1368,8 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, PV&
   }
   __syncthreads();
   const int m = min(sh.ints[4], kGenCap);
-  if (m <= kGenRankMax) {
-    // short lists: each entry's rank by counting (composites are distinct), through lpr's storage
-    const int mpad = (m + 15) & ~15;
-    for (int i = m + tid; i < mpad; i += kGenThreads) sh.list[i] = 0ull;
-    __syncthreads();
-    uint64_t* tmp = reinterpret_cast<uint64_t*>(sh.lpr);
-    for (int i = tid; i < m; i += kGenThreads) {
-      const uint64_t x = sh.list[i];
-      tmp[rank_count(sh.list, m, x)] = x;
-    }
-    __syncthreads();
-    for (int i = tid; i < m; i += kGenThreads) sh.list[i] = tmp[i];
-    __syncthreads();
-  } else {
-    int p2 = 1;
-    while (p2 < m) p2 <<= 1;
-    for (int i = m + tid; i < p2; i += kGenThreads) sh.list[i] = 0ull;
-    bitonic_desc<kGenThreads>(sh.list, p2);
-  }
-  // two entries per thread, inclusive prefix of weights
-  const int i0 = 2 * tid, i1 = i0 + 1;
-  const double w0 = i0 < m ? (MASS ? numer_g(g, comp_val(sh.list[i0])) : 1.0) : 0.0;
-  const double w1 = i1 < m ? (MASS ? numer_g(g, comp_val(sh.list[i1])) : 1.0) : 0.0;
-  double em;
-  uint32_t ec;
-  block_excl_scan<kGenThreads>(w0 + w1, 0u, em, ec, sh.wm, sh.wc);
-  if (i0 < kGenCap) sh.lpr[i0] = above + em + w0;
-  if (i1 < kGenCap) sh.lpr[i1] = above + em + w0 + w1;
-  if (tid == 0) sh.ints[5] = m;
-  __syncthreads();
-  const bool k0 = i0 < m && sh.lpr[i0] >= target, k1 = i1 < m && sh.lpr[i1] >= target;
-  wave_claim_min(&sh.ints[5], k0 || k1, k0 ? i0 : i1);
-  __syncthreads();
-  Sel s;
-  if (m == 0) {  // empty range (cannot happen for a bucket chosen by its count; kept defensive)
-    s.found = false;
-    s.ck = 0ull;
-    s.rank = rank_above;
-    s.before = s.incl = above;
-    __syncthreads();
-    return s;
-  }
-  int j = sh.ints[5];
-  s.found = j < m;
-  if (!s.found) j = m - 1;  // rounding left the target just past this range: its last element
-  s.ck = sh.list[j];
-  s.rank = rank_above + j;
-  s.before = j > 0 ? sh.lpr[j - 1] : above;
-  s.incl = sh.lpr[j];
-  __syncthreads();
-  return s;
+  sort_desc(sh, sh.list, reinterpret_cast<uint64_t*>(sh.lpr), m);
+  return scan_sorted<MASS>(g, sh, sh.list, sh.lpr, m, rank_above, above, target);
 }
 
 __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
@@ -1500,17 +1517,8 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   }
   const int keep_minp = keep;
 
-  // Mass select over the top-k prefix: level 0 = the mass bucket q, then composite refinement.
-  auto mass_select = [&](double target) -> Sel {
-    Sel s;
-    if (!(target > 0.0)) {  // the first element already reaches it (src/sampler.cpp:105-106)
-      s.found = true;
-      s.ck = mxc;
-      s.rank = 0;
-      s.before = 0.0;
-      s.incl = 1.0;
-      return s;
-    }
+  // The first non-empty level-0 bucket whose inclusive mass reaches target (kGenBuckets: none).
+  auto find_bucket = [&](double target) -> int {
     if (tid == 0) sh.ints[6] = kGenBuckets;
     __syncthreads();
     for (int b = tid; b < kGenBuckets; b += kGenThreads) {
@@ -1519,6 +1527,24 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     }
     __syncthreads();
     const int qb = sh.ints[6];
+    __syncthreads();
+    return qb;
+  };
+  auto first_element = [&]() -> Sel {  // the first element already reaches the target (src/sampler.cpp:105-106)
+    Sel s;
+    s.found = true;
+    s.ck = mxc;
+    s.rank = 0;
+    s.before = 0.0;
+    s.incl = 1.0;
+    return s;
+  };
+
+  // Mass select over the top-k prefix: level 0 = the mass bucket q, then composite refinement.
+  auto mass_select = [&](double target) -> Sel {
+    Sel s;
+    if (!(target > 0.0)) return first_element();
+    const int qb = find_bucket(target);
     if (qb == kGenBuckets) {
       s.found = false;
       s.ck = 0ull;
@@ -1551,10 +1577,14 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     return s;
   };
 
-  // src/sampler.cpp:92-100 (top-p): the first prefix whose share of `sum` reaches top_p
-  if (P.top_p > 0.0f && P.top_p < 1.0f) {
-    const double tp = static_cast<double>(P.top_p);
-    const Sel s = mass_select(tp * sum);
+  // src/sampler.cpp:101-108 draws u * tot over the kept prefix; u is taken first because, in the
+  // usual case below, the top-p cut and the draw share one pass over the row.
+  if (tid == 0) sh.dbls[1] = draw_u(a, row, P);
+  __syncthreads();
+  const double u = sh.dbls[1];
+  const bool topp = P.top_p > 0.0f && P.top_p < 1.0f;
+  const double tp = static_cast<double>(P.top_p);
+  auto apply_topp = [&](const Sel& s) {  // src/sampler.cpp:92-100
     const double mg = fmin(fabs(s.incl / sum - tp), fabs(s.before / sum - tp));
     if (mg < kNearTopP) flags |= VSMP_FLAG_TOPP_NEAR;
     if (s.found && s.rank + 1 < keep) {
@@ -1563,15 +1593,76 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       last = s.ck;
       last_from = 2;
     }
+  };
+  // Shared pass: when the top-p target's bucket qp lies wholly inside the kept prefix, the cut
+  // certainly lands in qp, so tot lies between the masses before and through qp, and the draw
+  // target u * tot between u times those: a bracket of level-0 buckets [d_lo, d_hi]. One pass then
+  // collects qp's elements (list A) and the bracket's (list B, whose sorted order keeps each bucket
+  // contiguous); each select runs on its bucket exactly as a pass of its own would.
+  bool shared = false, drawn = false;
+  Sel d;
+  double target = 0.0;
+  if (topp && tp * sum > 0.0 && u > 0.0) {
+    const double tgt = tp * sum;
+    const int qp = find_bucket(tgt);
+    if (qp < kGenBuckets) {
+      const int ra_p = qp > 0 ? static_cast<int>(sh.cnt0[qp - 1]) : 0;
+      const int n_p = static_cast<int>(sh.cnt0[qp]) - ra_p;
+      const double above_p = qp > 0 ? sh.mass0[qp - 1] : 0.0;
+      if (static_cast<int>(sh.cnt0[qp]) < keep && n_p <= kGenCap / 2 && u * above_p > 0.0) {
+        const int d_lo = find_bucket(u * above_p);
+        const int d_hi = find_bucket(u * sh.mass0[qp] * (1.0 + 1e-12));  // slack: tot's sum order differs
+        const int base_d = d_lo > 0 ? static_cast<int>(sh.cnt0[d_lo - 1]) : 0;
+        if (d_hi < kGenBuckets && static_cast<int>(sh.cnt0[d_hi]) - base_d <= kGenCap / 2) {
+          shared = true;
+          uint64_t* listA = sh.list;
+          uint64_t* listB = sh.list + kGenCap / 2;
+          double* lprA = sh.lpr;
+          double* lprB = sh.lpr + kGenCap / 2;
+          if (tid == 0) {
+            sh.ints[4] = 0;
+            sh.ints[7] = 0;
+          }
+          __syncthreads();
+          const uint64_t ckk = g.ckk;
+          gen_pass(g.R, [&](int e, float v) {
+            const int q = q_of(g, v);
+            const bool inA = q == qp, inB = q >= d_lo && q <= d_hi;
+            if (!inA && !inB) return;
+            const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
+            if (ck < ckk) return;
+            if (inA) {
+              const int p = atomicAdd(&sh.ints[4], 1);
+              if (p < kGenCap / 2) listA[p] = ck;
+            }
+            if (inB) {
+              const int p = atomicAdd(&sh.ints[7], 1);
+              if (p < kGenCap / 2) listB[p] = ck;
+            }
+          });
+          __syncthreads();
+          const int mA = min(sh.ints[4], kGenCap / 2), mB = min(sh.ints[7], kGenCap / 2);
+          sort_desc(sh, listA, reinterpret_cast<uint64_t*>(lprA), mA);
+          apply_topp(scan_sorted<true>(g, sh, listA, lprA, mA, ra_p, above_p, tgt));
+          target = u * tot;
+          const int qd = find_bucket(target);
+          if (qd >= d_lo && qd <= d_hi) {
+            sort_desc(sh, listB, reinterpret_cast<uint64_t*>(lprB), mB);
+            const int ra_d = qd > 0 ? static_cast<int>(sh.cnt0[qd - 1]) : 0;
+            const int n_d = static_cast<int>(sh.cnt0[qd]) - ra_d;
+            const double above_d = qd > 0 ? sh.mass0[qd - 1] : 0.0;
+            d = scan_sorted<true>(g, sh, listB + (ra_d - base_d), lprB + (ra_d - base_d), n_d, ra_d, above_d, target);
+            drawn = true;
+          }
+        }
+      }
+    }
   }
-
-  // src/sampler.cpp:101-108: inverse-CDF draw over the sorted draw set
-  double u = 0.0;
-  if (tid == 0) sh.dbls[1] = draw_u(a, row, P);
-  __syncthreads();
-  u = sh.dbls[1];
-  const double target = u * tot;
-  const Sel d = mass_select(target);
+  if (!shared && topp) apply_topp(mass_select(tp * sum));
+  if (!drawn) {
+    target = u * tot;
+    d = mass_select(target);
+  }
   if (last_from != 2 && (!(d.found && d.rank < keep) || a.info)) last = kept_last(last_from == 1);
   int id, rank;
   double margin;
