@@ -1857,18 +1857,28 @@ __device__ __forceinline__ void rows_general_prepass(const KArgs& a, int row, co
   const int V4 = (V + 3) >> 2;
   uint64_t b = 0ull;
   uint32_t mn = 0xFFFFFFFFu;
-  for (int f = tid; f < V4; f += kRowNT) {
-    const uint4 v = *reinterpret_cast<const uint4*>(rpu + 4 * f);
-    const uint32_t x[4] = {v.x, v.y, v.z, v.w};
+  // eight 16-byte groups per thread in flight (128 KB per workgroup); plain loads, since k_general
+  // reads the row again; every load is issued (clamped to the last group) before any is used
+  constexpr int U = 8;
+  const uint4* rp4 = reinterpret_cast<const uint4*>(rpu);
+  for (int f0 = 0; f0 < V4; f0 += U * kRowNT) {
+    uint4 vv[U];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int e = 4 * f + c;
-      if (e < V) {
-        float fv = __uint_as_float(x[c]);
-        if (pen && bit_of(bits, e)) fv = penalise(fv, P.repeat);
-        const uint32_t k = key_of(__float_as_uint(fv));
-        b = max64(b, comp(k, static_cast<uint32_t>(e)));
-        mn = min(mn, k);
+    for (int u = 0; u < U; ++u) vv[u] = rp4[min(f0 + u * kRowNT + tid, V4 - 1)];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int f = f0 + u * kRowNT + tid;
+      const uint32_t x[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int e = 4 * f + c;
+        if (e < V) {
+          float fv = __uint_as_float(x[c]);
+          if (pen && bit_of(bits, e)) fv = penalise(fv, P.repeat);
+          const uint32_t k = key_of(__float_as_uint(fv));
+          b = max64(b, comp(k, static_cast<uint32_t>(e)));
+          mn = min(mn, k);
+        }
       }
     }
   }
