@@ -1099,18 +1099,28 @@ constexpr int kRefBuckets = 2048;
 
 struct GenRow {
   const float* rp;
-  const uint32_t* bits;
+  const uint32_t* bits;  // the penalty bitmap in global memory
   int V;
   bool pen;
+  bool lds_bits;  // the bitmap has been copied to the dynamic LDS of k_general (gen_lds_bits())
   float rep;
 };
+
+// k_general's dynamic LDS: a copy of the row's penalty bitmap, when it fits (kGenBitsLds bytes).
+// Reading it from LDS keeps the per-element lookups off the vector memory counter, which retires in
+// order and would otherwise make each lookup wait for the row loads in flight behind it.
+constexpr size_t kGenBitsLds = 80 * 1024;
+__device__ __forceinline__ uint32_t* gen_lds_bits() {
+  extern __shared__ uint32_t gen_bits_dyn[];
+  return gen_bits_dyn;
+}
 
 // Calls f(index, value) for every element of the row, penalty applied. Two iterations of
 // loads in flight (a and b); every load is issued unconditionally (past the row it rereads the last
 // 16-byte group, which 4*ceil(V/4) <= ld keeps inside the row), so each wait covers exactly the
 // buffer about to be processed.
-template <class F>
-__device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
+template <class F, class W>
+__device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, W&& word) {
   constexpr int U = 1;
   constexpr int step = kGenThreads * 4 * U;
   const int tid = static_cast<int>(threadIdx.x);
@@ -1127,7 +1137,7 @@ __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
     for (int u = 0; u < U; ++u) {
       const int e = it * step + (u * kGenThreads + tid) * 4;
       if (e >= R.V) continue;
-      const uint32_t nib = R.pen ? (R.bits[e >> 5] >> (e & 31)) & 0xFu : 0u;
+      const uint32_t nib = R.pen ? (word(e >> 5) >> (e & 31)) & 0xFu : 0u;
       const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -1147,6 +1157,16 @@ __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
     if (it + 1 < nit) process(it + 1, b);
     load(it + 3, b);
   }
+}
+
+// Two loops rather than one with a chosen pointer: a pointer that may be LDS or global memory
+// becomes a flat load, which waits on the vector memory counter as well.
+template <class F>
+__device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
+  if (R.lds_bits)
+    gen_pass_loop(R, f, [](int i) { return gen_lds_bits()[i]; });
+  else
+    gen_pass_loop(R, f, [&R](int i) { return R.bits[i]; });
 }
 
 struct __align__(16) GenShared {  // list is read as 16-byte vectors
@@ -1401,6 +1421,13 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   g.R.pen = (P.repeat != 1.0f) && (h1 - h0) > 0;
   g.R.rep = P.repeat;
   g.R.bits = a.s_bits + static_cast<size_t>(row) * a.words;
+  g.R.lds_bits = false;
+  if (g.R.pen && static_cast<size_t>(a.words) * sizeof(uint32_t) <= kGenBitsLds) {  // the launch's rule
+    uint32_t* lb = gen_lds_bits();
+    for (int i = tid; i < a.words; i += kGenThreads) lb[i] = g.R.bits[i];
+    __syncthreads();
+    g.R.lds_bits = true;
+  }
   g.mx = comp_val(mxc);
   g.temp = P.temp;
   g.inv_temp = 1.0 / static_cast<double>(P.temp);
@@ -2380,7 +2407,15 @@ void launch_rows(const KArgs& a, hipStream_t st) {
 }
 
 void launch_general(const KArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_general, dim3(a.B), dim3(kGenThreads), 0, st, a);
+  const size_t bytes = static_cast<size_t>(a.words) * sizeof(uint32_t);
+  const size_t dyn = (a.hist_off != nullptr && bytes <= kGenBitsLds) ? bytes : 0;
+  static bool configured = false;
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_general), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(kGenBitsLds));
+    configured = true;
+  }
+  hipLaunchKernelGGL(k_general, dim3(a.B), dim3(kGenThreads), dyn, st, a);
 }
 
 }  // namespace vsmp
