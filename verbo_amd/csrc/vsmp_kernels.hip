@@ -20,6 +20,7 @@
 //            count and by fp64 mass over the row, with histograms in LDS.
 //  k_read_probe  a plain streaming read, for the attainable-bandwidth measurement.
 #include <cfloat>
+#include <type_traits>
 
 #include "vsmp_common.hpp"
 
@@ -1431,10 +1432,12 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   g.mx = comp_val(mxc);
   g.temp = P.temp;
   g.inv_temp = 1.0 / static_cast<double>(P.temp);
+  bool capped;  // the buckets stop short of the row minimum: the overflow bucket may hold most of it
   {
     float range = g.mx - key_val(static_cast<uint32_t>(mnk));
     const float cap = 64.0f * P.temp;
-    if (!(range <= cap)) range = cap;
+    capped = !(range <= cap);
+    if (capped) range = cap;
     g.qs = range > 0.0f ? static_cast<float>(kGenBuckets) / range : 0.0f;
   }
   const int k = top_k_of(P, V);
@@ -1465,21 +1468,43 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   __syncthreads();
   const bool minp = P.min_p > 0.0f;
   const double thr = static_cast<double>(P.min_p);  // pr of the maximum is exactly 1
-  double t_sum = 0.0, t_totm = 0.0;
-  uint32_t t_cntm = 0;
+  double t_sum = 0.0, t_totm = 0.0, t_omass = 0.0;
+  uint32_t t_cntm = 0, t_ocnt = 0;
   const bool cut_k = g.ckk != 0ull;
-  gen_pass(g.R, [&](int e, float v) {
-    if (cut_k && comp(ord_key(v), static_cast<uint32_t>(e)) < g.ckk) return;
-    const double p = numer_g(g, v);
-    t_sum += p;
-    if (minp && p >= thr) {
-      ++t_cntm;
-      t_totm += p;
+  // ovf: the overflow bucket (most of a cold row when capped) is summed per thread rather than by
+  // atomics that would all hit one address
+  auto main_pass = [&](auto ovf) {
+    gen_pass(g.R, [&](int e, float v) {
+      if (cut_k && comp(ord_key(v), static_cast<uint32_t>(e)) < g.ckk) return;
+      const double p = numer_g(g, v);
+      t_sum += p;
+      if (minp && p >= thr) {
+        ++t_cntm;
+        t_totm += p;
+      }
+      const int q = q_of(g, v);
+      if (decltype(ovf)::value && q == kGenBuckets - 1) {
+        ++t_ocnt;
+        t_omass += p;
+      } else {
+        atomicAdd(&sh.cnt0[q], 1u);
+        atomicAdd(&sh.mass0[q], p);
+      }
+    });
+  };
+  if (capped)
+    main_pass(std::true_type{});
+  else
+    main_pass(std::false_type{});
+  {
+    const uint32_t oc = block_sum_u32<kGenThreads>(t_ocnt, sh.r32);
+    const double om = block_sum_f64<kGenThreads>(t_omass, sh.rd);
+    if (tid == 0) {
+      sh.cnt0[kGenBuckets - 1] += oc;
+      sh.mass0[kGenBuckets - 1] += om;
     }
-    const int q = q_of(g, v);
-    atomicAdd(&sh.cnt0[q], 1u);
-    atomicAdd(&sh.mass0[q], p);
-  });
+    __syncthreads();
+  }
   const double sum = block_sum_f64<kGenThreads>(t_sum, sh.rd);
   double totm = 0.0;
   uint32_t cntm = 0;
