@@ -1395,11 +1395,33 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, PV&
 
 __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   __shared__ GenShared sh;
-  const int row = blockIdx.x;
-  const vsmp_params P = row_params(a, row);
   const int V = a.V;
-  if (path_of(P, V, a.smallk_ok) != kPathGeneral) return;
   const int tid = threadIdx.x;
+  // Workgroup b takes the b-th general row. With per-row parameters the general rows are then the
+  // first workgroups, which the dispatcher deals out evenly over the XCDs (one per CU at a time);
+  // by row index they could crowd one XCD into a second round.
+  int row = blockIdx.x;
+  if (a.params) {
+    if (tid == 0) sh.ints[0] = -1;
+    int base = 0;
+    for (int r0 = 0; r0 < a.B; r0 += kGenThreads) {
+      const int r = r0 + tid;
+      const bool gen = r < a.B && path_of(a.params[r], V, a.smallk_ok) == kPathGeneral;
+      double em;
+      uint32_t ec;
+      block_excl_scan<kGenThreads>(0.0, gen ? 1u : 0u, em, ec, sh.wm, sh.wc);
+      if (gen && base + static_cast<int>(ec) == static_cast<int>(blockIdx.x)) sh.ints[0] = r;
+      if (tid == kGenThreads - 1) sh.ints[1] = static_cast<int>(ec) + (gen ? 1 : 0);
+      __syncthreads();
+      base += sh.ints[1];
+      __syncthreads();
+    }
+    row = __builtin_amdgcn_readfirstlane(sh.ints[0]);
+    __syncthreads();
+    if (row < 0) return;  // fewer general rows than workgroups
+  }
+  const vsmp_params P = row_params(a, row);
+  if (path_of(P, V, a.smallk_ok) != kPathGeneral) return;
   const int S = a.S;
 
   // row maximum / minimum from the slices
