@@ -1263,6 +1263,9 @@ __device__ __forceinline__ void sort_desc(GenShared& sh, uint64_t* list, uint64_
   }
 }
 
+__device__ __forceinline__ Sel find_in_prefix(GenShared& sh, const uint64_t* list, const double* lpr, int m,
+                                              int rank_above, double above, double target);
+
 // The first entry of the descending list[0, m) at which the running weight, starting from `above`
 // after `rank_above` elements, reaches target. Weights are 1 (count) or the fp64 numerators (mass);
 // lpr[0, m) receives the inclusive running weights. When rounding leaves the target just past the
@@ -1279,6 +1282,14 @@ __device__ __forceinline__ Sel scan_sorted(const GenCtx& g, GenShared& sh, const
   block_excl_scan<kGenThreads>(w0 + w1, 0u, em, ec, sh.wm, sh.wc);
   if (i0 < m) lpr[i0] = above + em + w0;
   if (i1 < m) lpr[i1] = above + em + w0 + w1;
+  return find_in_prefix(sh, list, lpr, m, rank_above, above, target);
+}
+
+// The first entry of list[0, m) whose inclusive running weight lpr reaches target (see scan_sorted).
+__device__ __forceinline__ Sel find_in_prefix(GenShared& sh, const uint64_t* list, const double* lpr, int m,
+                                              int rank_above, double above, double target) {
+  const int tid = threadIdx.x;
+  const int i0 = 2 * tid, i1 = i0 + 1;
   if (tid == 0) sh.ints[5] = m;
   __syncthreads();
   const bool k0 = i0 < m && lpr[i0] >= target, k1 = i1 < m && lpr[i1] >= target;
@@ -1676,7 +1687,37 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   bool shared = false, drawn = false;
   Sel d;
   double target = 0.0;
-  if (topp && tp * sum > 0.0 && u > 0.0) {
+  // Small min-p prefix: its elements (numerator >= thr, all of them close to the maximum) are
+  // collected whole in one pass, numerators taken only above a float floor below the cut; the
+  // top-p cut and the draw are then taken on the sorted prefix sums.
+  if (minp && cntm >= 1u && cntm <= static_cast<uint32_t>(kGenCap)) {
+    const float vlo = g.mx + static_cast<float>(static_cast<double>(P.temp) * log(thr) * 1.001) - 1e-3f;
+    if (tid == 0) sh.ints[4] = 0;
+    __syncthreads();
+    gen_pass(g.R, [&](int e, float v) {
+      if (!(v >= vlo)) return;
+      if (!(numer_g(g, v) >= thr)) return;
+      const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
+      if (ck < g.ckk) return;
+      const int p = atomicAdd(&sh.ints[4], 1);
+      if (p < kGenCap) sh.list[p] = ck;
+    });
+    __syncthreads();
+    const int m = sh.ints[4];
+    __syncthreads();
+    if (m == static_cast<int>(cntm)) {  // every kept element collected (else: the passes below)
+      sort_desc(sh, sh.list, reinterpret_cast<uint64_t*>(sh.lpr), m);
+      const Sel s = scan_sorted<true>(g, sh, sh.list, sh.lpr, m, 0, 0.0, topp ? tp * sum : INFINITY);
+      tot = sh.lpr[m - 1];
+      last = sh.list[m - 1];
+      last_from = 2;
+      if (topp) apply_topp(s);
+      target = u * tot;
+      d = find_in_prefix(sh, sh.list, sh.lpr, keep, 0, 0.0, target);
+      shared = drawn = true;
+    }
+  }
+  if (!shared && topp && tp * sum > 0.0 && u > 0.0) {
     const double tgt = tp * sum;
     const int qp = find_bucket(tgt);
     if (qp < kGenBuckets) {
