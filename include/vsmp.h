@@ -73,6 +73,10 @@ typedef struct {
                                   fp64 sums instead */
 #define VSMP_FLAG_CUTS_DIFFER 32u /* diagnostics only (info requested): the parallel decision and
                                      the sequential one differed; never expected */
+#define VSMP_FLAG_ONE_PASS 64u    /* general path: the top-p cut and the draw were taken from one
+                                     pass over the row (the cut's bucket bounded the draw's) */
+#define VSMP_FLAG_MINP_PREFIX 128u /* general path: the min-p prefix was collected whole in one
+                                      pass, and the cut and the draw taken on its sorted sums */
 
 typedef struct vsmp_ctx vsmp_ctx;
 

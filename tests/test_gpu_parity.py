@@ -235,3 +235,56 @@ def test_counter_seeds_with_shared_params(ctx, mode):
         u = np.array([O.counter_u(int(p["seed"]) + r, counter) for r in range(w.B)])
         o = O.pick_rows(w.logits, w.params, w.hist, w.hist_off, u)[0]
         assert (ids == o).all()
+
+
+def _general_batch(rng, kind, B=24, Vv=30000):
+    """Rows that take the general path (top-k off) and one of its pass plans."""
+    p = np.zeros(B, V.SAMPLING_DTYPE)
+    p["top_k"] = 0
+    p["repeat"] = 1.0
+    p["seed"] = rng.integers(1, 1 << 62, B)
+    hists = [[] for _ in range(B)]
+    if kind == "flat":  # the cut's bucket bounds the draw's: one shared pass
+        lg = rng.normal(0, 0.5, (B, Vv))
+        p["temp"] = 1.0
+        p["top_p"] = rng.choice([0.9, 0.95, 0.99], B)
+    elif kind == "minp":  # a few spikes hold the min-p prefix: collected whole
+        lg = rng.normal(0, 2.0, (B, Vv))
+        for r in range(B):
+            lg[r, rng.integers(0, Vv, 8)] += 6.0 + 2.0 * rng.random(8)
+        p["temp"] = rng.choice([0.5, 0.7, 1.0], B)
+        p["top_p"] = rng.choice([0.8, 0.9, 1.0], B)
+        p["min_p"] = rng.choice([0.05, 0.1], B)
+        p["repeat"] = 1.2
+        hists = [rng.integers(0, Vv, int(rng.integers(0, 200))) for _ in range(B)]
+    elif kind == "cold":  # the buckets stop far short of the minimum: the overflow bucket holds most rows
+        lg = rng.normal(0, 2.0, (B, Vv))
+        p["temp"] = rng.choice([0.005, 0.02, 0.05], B)
+        p["top_p"] = rng.choice([0.95, 1.0], B)
+    else:  # general and small-k rows interleaved, per-row parameters: workgroups renumber the general rows
+        lg = rng.normal(0, 1.5, (B, Vv))
+        p["temp"] = rng.choice([0.0, 0.6, 1.1], B)
+        p["top_k"] = rng.choice([0, 0, 40, 300], B)
+        p["top_p"] = rng.choice([0.9, 1.0], B)
+        p["min_p"] = rng.choice([0.0, 0.05], B)
+        p["repeat"] = rng.choice([1.0, 1.3], B)
+        hists = [rng.integers(0, Vv, int(rng.integers(0, 500))) for _ in range(B)]
+    h, off = csr(hists)
+    return lg.astype(np.float32), p, h, off
+
+
+@pytest.mark.parametrize("kind", ["flat", "minp", "cold", "interleaved"])
+def test_general_path_pass_plans(ctx, mode, kind):
+    rng = np.random.default_rng({"flat": 11, "minp": 12, "cold": 13, "interleaved": 14}[kind])
+    lg, p, h, off = _general_batch(rng, kind)
+    log("general pass plan", mode, kind)
+    run = Run(ctx, lg, p, h, off)
+    run.report()
+    gen = run.info["path"] == V.PATH_GENERAL
+    flags = run.info["flags"][gen]
+    if kind == "flat":
+        assert (flags & V.FLAG_ONE_PASS).mean() >= 0.5, flags
+    if kind == "minp":
+        assert (flags & V.FLAG_MINP_PREFIX).mean() >= 0.5, flags
+    if kind == "interleaved":
+        assert gen.any() and (~gen).any()

@@ -24,6 +24,7 @@ __version__ = "0.1.0"
 U_SUPPLIED, U_COUNTER, U_XORSHIFT = 0, 1, 2
 FLAG_TOPP_NEAR, FLAG_MINP_NEAR, FLAG_DRAW_NEAR, FLAG_FALLBACK = 1, 2, 4, 8
 FLAG_SEQ_CUTS, FLAG_CUTS_DIFFER = 16, 32
+FLAG_ONE_PASS, FLAG_MINP_PREFIX = 64, 128
 PATH_GREEDY, PATH_SMALLK, PATH_GENERAL = 0, 1, 2
 
 

@@ -1715,6 +1715,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       target = u * tot;
       d = find_in_prefix(sh, sh.list, sh.lpr, keep, 0, 0.0, target);
       shared = drawn = true;
+      flags |= VSMP_FLAG_MINP_PREFIX;
     }
   }
   if (!shared && topp && tp * sum > 0.0 && u > 0.0) {
@@ -1768,6 +1769,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
             const double above_d = qd > 0 ? sh.mass0[qd - 1] : 0.0;
             d = scan_sorted<true>(g, sh, listB + (ra_d - base_d), lprB + (ra_d - base_d), n_d, ra_d, above_d, target);
             drawn = true;
+            flags |= VSMP_FLAG_ONE_PASS;
           }
         }
       }
