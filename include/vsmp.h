@@ -127,6 +127,11 @@ VSMP_API int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsm
  * the attainable HBM read bandwidth that the sampler's roofline is compared with. Returns 0 or -1. */
 VSMP_API int vsmp_read_probe(vsmp_ctx* ctx, const void* p, long long bytes, void* stream);
 
+/* Diagnostics, no reference counterpart: y[i] = the fp64 exp that the general path (top-k off or
+ * above 256) uses for its numerators, for i < n, on `stream` (x, y: device arrays of n doubles).
+ * Its accuracy against exp is what the tests bound. Returns 0 or -1. */
+VSMP_API int vsmp_exp_probe(vsmp_ctx* ctx, const double* x, double* y, long long n, void* stream);
+
 /* A drop-in sampler object: verbo::Sampler (reference include/verbo/verbo.hpp:116-132) behind
  * a C handle, for FFI callers. Its history, xorshift stream and seeding are the reference's
  * (src/sampler.cpp:24-48); pick runs on the GPU through the calling thread's context. */

@@ -288,3 +288,24 @@ def test_general_path_pass_plans(ctx, mode, kind):
         assert (flags & V.FLAG_MINP_PREFIX).mean() >= 0.5, flags
     if kind == "interleaved":
         assert gen.any() and (~gen).any()
+
+
+def test_general_path_exp_accuracy(ctx):
+    """The general path's fp64 exp (a 64-entry table method) against exp in long double: within
+    1.01 ulp over [-745, 0] (the reference's libm exp is within one ulp too), exactly 1 at 0 and 0
+    where exp underflows or the argument is -inf."""
+    import torch
+
+    rng = np.random.default_rng(21)
+    x = np.concatenate([-745.0 * rng.random(300000), -40.0 * rng.random(300000), -rng.random(300000),
+                        -0.01 * rng.random(300000), -np.arange(0.0, 745.0, 0.125),
+                        np.array([0.0, -0.0, -5e-324, -1e-300, -708.0, -708.5, -744.0])])
+    y = ctx.exp_probe(torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = np.exp(x.astype(np.longdouble))
+    ulp = np.spacing(ref.astype(np.float64)).astype(np.longdouble)
+    err = np.abs(y.astype(np.longdouble) - ref) / ulp
+    worst = int(np.argmax(err))
+    assert err[worst] <= 1.01, (x[worst], y[worst], ref[worst], float(err[worst]))
+    assert y[x == 0.0].tolist() == [1.0] * int((x == 0.0).sum())
+    special = ctx.exp_probe(torch.tensor([-746.0, -1e5, -np.inf], dtype=torch.float64, device="cuda")).cpu().numpy()
+    assert special.tolist() == [0.0, 0.0, 0.0]

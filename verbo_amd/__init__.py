@@ -121,6 +121,7 @@ def load_library():
         "vsmp_sampler_accept": (None, [_P, ctypes.c_int]),
         "vsmp_sampler_reset": (None, [_P]),
         "vsmp_read_probe": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P]),
+        "vsmp_exp_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_longlong, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -242,6 +243,19 @@ class Context:
         nbytes = t.numel() * t.element_size() // 16 * 16
         if _lib.vsmp_read_probe(self._h, t.data_ptr(), nbytes, ctypes.c_void_p(st.cuda_stream)) != 0:
             raise _err()
+
+    def exp_probe(self, x, stream=None):
+        """vsmp_exp_probe: the general path's fp64 exp over device tensor `x` (float64); returns y."""
+        import torch
+
+        if x.dtype != torch.float64 or not x.is_cuda:
+            raise VsmpError("exp_probe needs a float64 device tensor")
+        x = x.contiguous()
+        y = torch.empty_like(x)
+        st = stream if stream is not None else torch.cuda.current_stream(x.device)
+        if _lib.vsmp_exp_probe(self._h, x.data_ptr(), y.data_ptr(), x.numel(), ctypes.c_void_p(st.cuda_stream)) != 0:
+            raise _err()
+        return y
 
     def pick_host(self, logits, params, hist=(), u=0.0, with_info=False):
         """vsmp_pick_host: one pick on a host row (numpy). Returns id (and RowInfo)."""

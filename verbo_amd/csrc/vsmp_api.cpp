@@ -358,4 +358,14 @@ int vsmp_read_probe(vsmp_ctx* ctx, const void* p, long long bytes, void* stream)
   return vsmp::hip_ok(hipGetLastError(), "read-probe launch") ? 0 : -1;
 }
 
+int vsmp_exp_probe(vsmp_ctx* ctx, const double* x, double* y, long long n, void* stream) {
+  vsmp::clear_error();
+  if (!ctx || (n > 0 && (!x || !y))) return vsmp::set_error("vsmp: null argument");
+  if (n < 0) return vsmp::set_error("vsmp: exp probe needs n >= 0");
+  if (n == 0) return 0;
+  if (!vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  vsmp::launch_exp_probe(x, y, n, static_cast<hipStream_t>(stream));
+  return vsmp::hip_ok(hipGetLastError(), "exp-probe launch") ? 0 : -1;
+}
+
 }  // extern "C"

@@ -62,5 +62,6 @@ void launch_finish(const KArgs& a, hipStream_t st);
 void launch_rows(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
 void launch_read_probe(const void* p, long long n16, unsigned* sink, int grid, hipStream_t st);
+void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st);
 
 }  // namespace vsmp

@@ -19,6 +19,8 @@
 //  k_general one workgroup per remaining row (k > 256 or top-k off): multi-pass radix select by
 //            count and by fp64 mass over the row, with histograms in LDS.
 //  k_read_probe  a plain streaming read, for the attainable-bandwidth measurement.
+//  k_exp_probe   the general path's fp64 exp over an array, for measuring its accuracy.
+#include <algorithm>
 #include <cfloat>
 #include <type_traits>
 
@@ -1211,12 +1213,62 @@ struct GenCtx {
   uint64_t ckk;  // top-k restriction: element in the prefix iff composite >= ckk
 };
 
+// 2^(j/64), j = 0..63, rounded to nearest.
+constexpr double kExp2J64[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0};
+
+// The LDS copy of kExp2J64 that exp_tab reads; a kernel calls exp_tab_fill, then a barrier, first.
+__device__ __forceinline__ double* exp_tab_lds() {
+  __shared__ double tab[64];
+  return tab;
+}
+__device__ __forceinline__ void exp_tab_fill() {
+  if (threadIdx.x < 64) exp_tab_lds()[threadIdx.x] = kExp2J64[threadIdx.x];
+}
+
+// exp(x) in fp64 by P. T. P. Tang's table-driven method (ACM TOMS 15(2):144-157, 1989) with 64
+// table entries: x = (64 m + j) ln2/64 + r, |r| <= ln2/128 (ln2/64 split in two for the
+// reduction), exp(x) = 2^m * 2^(j/64) * (1 + p(r)), p the degree-6 Taylor polynomial of e^r - 1
+// (truncation below 3e-20). Within 1.01 ulp of exp(x) over [-745, 0]; about 15 instructions
+// against the library routine's 30. x is clamped at -1000 first, so -inf (and NaN) give 0.
+__device__ __forceinline__ double exp_tab(double x) {
+  x = fmax(x, -1000.0);
+  const double n = rint(x * 0x1.71547652b82fep+6);  // 64 / ln2
+  double r = fma(-n, 0x1.62e42fefa39efp-7, x);      // ln2/64, leading part
+  r = fma(-n, 0x1.abc9e3b39803fp-62, r);            // ... trailing part
+  double q = fma(r, 0x1.6c16c16c16c17p-10, 0x1.1111111111111p-7);  // 1/720, 1/120
+  q = fma(r, q, 0x1.5555555555555p-5);  // 1/24
+  q = fma(r, q, 0x1.5555555555555p-3);  // 1/6
+  q = fma(r, q, 0.5);
+  q = fma(r, q, 1.0);
+  const double p = r * q;
+  const int ni = static_cast<int>(n);
+  const double t = exp_tab_lds()[ni & 63];
+  return ldexp(fma(t, p, t), ni >> 6);
+}
+
 // The general path's numerator, exp(double(float(v - mx)) * (1 / temp)): the reference divides by
-// temp (src/sampler.cpp:83); the product differs by at most an ulp of the exponent argument, far
-// inside the tolerance this path is held to (its cuts are taken on fp64 sums in bucket order and
-// compared with the reference's margins). One function for every sum the path takes.
+// temp (src/sampler.cpp:83); the product differs by at most an ulp of the exponent argument, and
+// exp_tab from the reference's exp by about an ulp, far inside the tolerance this path is held to
+// (its cuts are taken on fp64 sums in bucket order and compared with the reference's margins).
+// One function for every sum the path takes.
 __device__ __forceinline__ double numer_g(const GenCtx& g, float v) {
-  return exp(static_cast<double>(v - g.mx) * g.inv_temp);
+  return exp_tab(static_cast<double>(v - g.mx) * g.inv_temp);
 }
 
 __device__ __forceinline__ int q_of(const GenCtx& g, float v) {
@@ -1434,6 +1486,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   const vsmp_params P = row_params(a, row);
   if (path_of(P, V, a.smallk_ok) != kPathGeneral) return;
   const int S = a.S;
+  exp_tab_fill();  // ordered before its first use by the barriers of the reductions below
 
   // row maximum / minimum from the slices
   uint64_t mxc = 0ull, mnk = ~0ull;
@@ -2461,7 +2514,20 @@ __global__ __launch_bounds__(256) void k_read_probe(const uint4* __restrict__ p,
   if (acc == 0x9E3779B9u) sink[blockIdx.x & 7] = acc;  // keeps the loads; the value is not used
 }
 
+// Diagnostics: y[i] = exp_tab(x[i]), the general path's exp, for measuring its accuracy.
+__global__ __launch_bounds__(256) void k_exp_probe(const double* __restrict__ x, double* __restrict__ y, long long n) {
+  exp_tab_fill();
+  __syncthreads();
+  const long long stride = static_cast<long long>(gridDim.x) * 256;
+  for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) y[i] = exp_tab(x[i]);
+}
+
 }  // namespace
+
+void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st) {
+  const long long blocks = std::min<long long>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(k_exp_probe, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, x, y, n);
+}
 
 void launch_read_probe(const void* p, long long n16, unsigned* sink, int grid, hipStream_t st) {
   hipLaunchKernelGGL(k_read_probe, dim3(grid), dim3(256), 0, st, static_cast<const uint4*>(p), n16, sink);
