@@ -1122,8 +1122,8 @@ __device__ __forceinline__ uint32_t* gen_lds_bits() {
 // loads in flight (a and b); every load is issued unconditionally (past the row it rereads the last
 // 16-byte group, which 4*ceil(V/4) <= ld keeps inside the row), so each wait covers exactly the
 // buffer about to be processed.
-template <class F, class W>
-__device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, W&& word) {
+template <class F, class F4, class W>
+__device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, F4&& f4, W&& word) {
   constexpr int U = 1;
   constexpr int step = kGenThreads * 4 * U;
   const int tid = static_cast<int>(threadIdx.x);
@@ -1140,15 +1140,21 @@ __device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, W&& word) 
     for (int u = 0; u < U; ++u) {
       const int e = it * step + (u * kGenThreads + tid) * 4;
       if (e >= R.V) continue;
-      const uint32_t nib = R.pen ? (word(e >> 5) >> (e & 31)) & 0xFu : 0u;
-      const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      if (R.pen) {
+        const uint32_t nib = (word(e >> 5) >> (e & 31)) & 0xFu;
+        if (nib) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (e + c < R.V) {
-          float fv = x[c];
-          if (nib & (1u << c)) fv = penalise(fv, R.rep);
-          f(e + c, fv);
+          for (int c = 0; c < 4; ++c)
+            if (nib & (1u << c)) x[c] = penalise(x[c], R.rep);
         }
+      }
+      if (e + 4 <= R.V) {
+        f4(e, x);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (e + c < R.V) f(e + c, x[c]);
       }
     }
   };
@@ -1164,12 +1170,21 @@ __device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, W&& word) 
 
 // Two loops rather than one with a chosen pointer: a pointer that may be LDS or global memory
 // becomes a flat load, which waits on the vector memory counter as well.
+// f(index, value) is called per element; f4(index of the first, values[4]) for each whole
+// 16-byte group, which lets a caller order the work of four elements itself.
+template <class F, class F4>
+__device__ __forceinline__ void gen_pass_groups(const GenRow& R, F&& f, F4&& f4) {
+  if (R.lds_bits)
+    gen_pass_loop(R, f, f4, [](int i) { return gen_lds_bits()[i]; });
+  else
+    gen_pass_loop(R, f, f4, [&R](int i) { return R.bits[i]; });
+}
 template <class F>
 __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
-  if (R.lds_bits)
-    gen_pass_loop(R, f, [](int i) { return gen_lds_bits()[i]; });
-  else
-    gen_pass_loop(R, f, [&R](int i) { return R.bits[i]; });
+  gen_pass_groups(R, f, [&f](int e, const float (&x)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) f(e + c, x[c]);
+  });
 }
 
 struct __align__(16) GenShared {  // list is read as 16-byte vectors
@@ -1558,13 +1573,14 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   uint32_t t_cntm = 0, t_ocnt = 0;
   const bool cut_k = g.ckk != 0ull;
   // ovf: the overflow bucket (most of a cold row when capped) is summed per thread rather than by
-  // atomics that would all hit one address
-  auto main_pass = [&](auto ovf) {
-    gen_pass(g.R, [&](int e, float v) {
-      if (cut_k && comp(ord_key(v), static_cast<uint32_t>(e)) < g.ckk) return;
-      const double p = numer_g(g, v);
+  // atomics that would all hit one address; with_minp: the min-p statistics are taken
+  auto main_pass = [&](auto ovf, auto with_minp, auto with_cut) {
+    auto excluded = [&](int e, float v) {
+      return decltype(with_cut)::value && cut_k && comp(ord_key(v), static_cast<uint32_t>(e)) < g.ckk;
+    };
+    auto add = [&](float v, double p) {
       t_sum += p;
-      if (minp && p >= thr) {
+      if (decltype(with_minp)::value && minp && p >= thr) {
         ++t_cntm;
         t_totm += p;
       }
@@ -1576,12 +1592,35 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
         atomicAdd(&sh.cnt0[q], 1u);
         atomicAdd(&sh.mass0[q], p);
       }
-    });
+    };
+    gen_pass_groups(
+        g.R,
+        [&](int e, float v) {
+          if (!excluded(e, v)) add(v, numer_g(g, v));
+        },
+        // the four numerators first: their exp-table reads then go out together, ahead of the
+        // histogram atomics (LDS writes, which later LDS reads may not pass)
+        [&](int e, const float (&x)[4]) {
+          double p[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) p[c] = numer_g(g, x[c]);
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (!excluded(e + c, x[c])) add(x[c], p[c]);
+        });
   };
-  if (capped)
-    main_pass(std::true_type{});
+  // one instance per combination without a top-k restriction (the common case: no per-element
+  // branches beyond the ones asked for); rows with one share an instance
+  if (cut_k)
+    main_pass(std::true_type{}, std::true_type{}, std::true_type{});
+  else if (capped && minp)
+    main_pass(std::true_type{}, std::true_type{}, std::false_type{});
+  else if (capped)
+    main_pass(std::true_type{}, std::false_type{}, std::false_type{});
+  else if (minp)
+    main_pass(std::false_type{}, std::true_type{}, std::false_type{});
   else
-    main_pass(std::false_type{});
+    main_pass(std::false_type{}, std::false_type{}, std::false_type{});
   {
     const uint32_t oc = block_sum_u32<kGenThreads>(t_ocnt, sh.r32);
     const double om = block_sum_f64<kGenThreads>(t_omass, sh.rd);
