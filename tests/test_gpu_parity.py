@@ -17,10 +17,11 @@ pytestmark = pytest.mark.gpu
 KAT = np.array([0.1, 3.0, 2.9, -1.0, 0.0], np.float32)
 
 
-@pytest.fixture(params=["slices", "rows"])
+@pytest.fixture(params=["slices", "rows", "split"])
 def mode(request, monkeypatch):
-    """Both decompositions on the same inputs: split rows (slices + merge) and one workgroup per
-    row. The library reads VSMP_MODE on every call."""
+    """Each decomposition on the same inputs: slices + merge, one workgroup per row, and (for
+    greedy batches with shared parameters; other batches take the default) rows cut into parts
+    finished by their last part. The library reads VSMP_MODE on every call."""
     monkeypatch.setenv("VSMP_MODE", request.param)
     return request.param
 
@@ -309,3 +310,35 @@ def test_general_path_exp_accuracy(ctx):
     assert y[x == 0.0].tolist() == [1.0] * int((x == 0.0).sum())
     special = ctx.exp_probe(torch.tensor([-746.0, -1e5, -np.inf], dtype=torch.float64, device="cuda")).cpu().numpy()
     assert special.tolist() == [0.0, 0.0, 0.0]
+
+
+@pytest.mark.parametrize("dmode", ["split", "rows"])
+def test_greedy_split_parts(ctx, monkeypatch, dmode):
+    """Greedy batches cut into parts (one launch, the last part of a row writes its id) against the
+    oracle and against one workgroup per row: ties of the maximum in different parts (the lowest
+    index wins), the maximum itself penalised, parts that end inside a 16-byte group or hold no
+    group, consecutive calls reusing the per-row slots, and a call without diagnostics."""
+    import torch
+
+    monkeypatch.setenv("VSMP_MODE", dmode)
+    rng = np.random.default_rng(31)
+    for B, Vv in [(1, 49152), (3, 1001), (5, 4097), (2, 20001), (17, 151936), (9, 131075), (40, 2052)]:
+        lg = rng.normal(0, 3, (B, Vv)).astype(np.float32)
+        for r in range(B):
+            lg[r, rng.choice(Vv, size=3, replace=False)] = lg[r].max() + 1.0
+        hists = [list(rng.integers(-2, Vv + 2, int(rng.integers(0, 600)))) + [int(np.argmax(lg[r]))]
+                 for r in range(B)]
+        h, off = csr(hists)
+        p = V.params_array(n=1, temp=0.0, top_k=40, top_p=0.9, repeat=1.3, repeat_last=0, seed=1)
+        log("greedy split", dmode, B, Vv)
+        run = Run(ctx, lg, p, h, off)
+        run.report()
+        assert (run.info["path"] == V.PATH_GREEDY).all()
+        for r in range(B):
+            hh = np.asarray(hists[r])
+            assert run.info["n_pen"][r] == len(np.unique(hh[(hh >= 0) & (hh < Vv)])), r
+    d = torch.from_numpy(lg).cuda()
+    pr = V.Params(*[p[0][f].item() for f in V.SAMPLING_DTYPE.names])
+    out = ctx.pick_batch(d, pr, torch.from_numpy(h).cuda(), torch.from_numpy(off).cuda())
+    torch.cuda.synchronize()
+    assert (out.cpu().numpy() == run.o_ids).all()

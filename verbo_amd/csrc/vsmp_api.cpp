@@ -82,6 +82,13 @@ struct vsmp_ctx {
   size_t n_min = 0;
   unsigned int* s_bits = nullptr;
   size_t n_bits = 0;
+  // split greedy rows: per-row slot, ticket and penalised-id count, zero between calls
+  unsigned long long* g_slot = nullptr;
+  size_t n_slot = 0;
+  unsigned int* g_tick = nullptr;
+  size_t n_tick = 0;
+  unsigned int* g_npen = nullptr;
+  size_t n_gnpen = 0;
   // host-pointer path buffers
   float* d_logits = nullptr;
   size_t n_logits = 0;
@@ -101,19 +108,43 @@ namespace vsmp {
 namespace {
 
 struct Plan {
-  bool rows;  // row mode: one workgroup per row (k_rows), else slices (k_stage1 + k_finish)
+  bool rows;   // row mode: one workgroup per row (k_rows), else slices (k_stage1 + k_finish)
+  bool split;  // a small greedy batch: each row cut into P parts in one launch (k_greedy_split)
+  int P;
   int ept, S, L, grid, xcd, smallk_ok;
   bool any_general, any_smallk, any_finish;
 };
 
-// VSMP_MODE=rows|slices pins the decomposition (testing and tuning); default: rows whenever the
-// vocabulary fits the row kernel (V <= 2^19), slices beyond.
+// VSMP_MODE=rows|slices|split pins the decomposition (testing and tuning); default: split parts
+// for a greedy batch of at most half as many rows as CUs, else rows whenever the vocabulary fits
+// the row kernel (V <= 2^19), slices beyond. split applies to greedy batches with shared
+// parameters only; other batches take the default.
 int forced_mode() {
   const char* e = std::getenv("VSMP_MODE");
   if (!e) return -1;
   if (std::strcmp(e, "rows") == 0) return 1;
   if (std::strcmp(e, "slices") == 0) return 0;
+  if (std::strcmp(e, "split") == 0) return 2;
   return -1;
+}
+
+// Parts per row of a split greedy batch: enough workgroups for two per CU, at most
+// kSplitMaxPartGroups 16-byte groups per part (all its loads in flight at once), at least 512
+// groups per part (one per thread). 0: no split.
+int split_parts(int B, int V, int cus, bool forced) {
+  const long long V4 = (static_cast<long long>(V) + 3) / 4;
+  const long long pmin = (V4 + kSplitMaxPartGroups - 1) / kSplitMaxPartGroups;
+  const long long pcus = (2LL * cus + B - 1) / B;
+  const long long pmax = std::max(pmin, V4 / 512);
+  // VSMP_SPLIT_P pins the parts per row (tuning), within [pmin, pmax]
+  static const long long forced_p = [] {
+    const char* e = std::getenv("VSMP_SPLIT_P");
+    return e ? std::atoll(e) : 0LL;
+  }();
+  const long long P = forced_p > 0 ? std::min(std::max(forced_p, pmin), pmax) : std::min(std::max(pmin, pcus), pmax);
+  if (!forced && (2LL * B > cus || P < 2)) return 0;
+  if (static_cast<long long>(B) * P > INT32_MAX) return 0;
+  return static_cast<int>(std::max<long long>(P, 1));
 }
 
 // Slice shape: enough workgroups to fill the chip (>= 2048), slices of 256*EPT elements, and no
@@ -121,6 +152,17 @@ int forced_mode() {
 Plan plan(int B, int V, const vsmp_params* hostp, int cus) {
   Plan pl{};
   const int fm = forced_mode();
+  if (hostp && path_host(*hostp, V, true) == kPathGreedy && (fm == -1 || fm == 2)) {
+    const int P = split_parts(B, V, cus, fm == 2);
+    if (P > 0) {
+      pl.split = true;
+      pl.P = P;
+      pl.S = 1;
+      pl.L = V;
+      pl.grid = B * P;
+      return pl;
+    }
+  }
   // One workgroup per row whenever the row fits its LDS bitmap: measured faster than slices plus a
   // merge kernel at every workload shape here, batch 1 included (14 vs 20 us at 1 x 49152).
   pl.rows = V <= kRowMaxVocab && fm != 0;
@@ -244,6 +286,18 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   a.s_min = ctx->s_min;
   a.s_bits = ctx->s_bits;
   a.words = words;
+  if (pl.split) {
+    if (!grow(ctx->g_slot, ctx->n_slot, static_cast<size_t>(B), true, "scratch") ||
+        !grow(ctx->g_tick, ctx->n_tick, static_cast<size_t>(B), true, "scratch") ||
+        !grow(ctx->g_npen, ctx->n_gnpen, static_cast<size_t>(B), true, "scratch"))
+      return -1;
+    a.P = pl.P;
+    a.g_slot = ctx->g_slot;
+    a.g_tick = ctx->g_tick;
+    a.g_npen = ctx->g_npen;
+    launch_greedy_split(a, st);
+    return hip_ok(hipGetLastError(), "split launch") ? 0 : -1;
+  }
   if (pl.rows) {
     launch_rows(a, st);
     if (!hip_ok(hipGetLastError(), "row launch")) return -1;
@@ -291,8 +345,8 @@ void vsmp_ctx_free(vsmp_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
-  void* bufs[] = {c->s_cand, c->s_cnt, c->s_npen, c->s_max, c->s_min, c->s_bits,
-                  c->d_logits, c->d_hist, c->d_hoff, c->d_u, c->d_out, c->d_info};
+  void* bufs[] = {c->s_cand, c->s_cnt, c->s_npen, c->s_max, c->s_min, c->s_bits, c->g_slot, c->g_tick,
+                  c->g_npen, c->d_logits, c->d_hist, c->d_hoff, c->d_u, c->d_out, c->d_info};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->stream) (void)hipStreamDestroy(c->stream);

@@ -55,13 +55,22 @@ struct KArgs {
   unsigned int* s_min;         // [B*S] slice minimum (order key)
   unsigned int* s_bits;        // [B][words] penalty bitmaps of general-path rows
   int words;                   // bitmap words per row
+  // split greedy rows: P parts per row; per-row slot (largest composite), ticket and penalised-id
+  // count, all zero between calls (the last part of a row clears them)
+  int P;
+  unsigned long long* g_slot;
+  unsigned int* g_tick;
+  unsigned int* g_npen;
 };
+
+constexpr int kSplitMaxPartGroups = 4096;  // 16-byte groups one split part loads (all in flight)
 
 void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st);
 void launch_finish(const KArgs& a, hipStream_t st);
 void launch_rows(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
 void launch_read_probe(const void* p, long long n16, unsigned* sink, int grid, hipStream_t st);
+void launch_greedy_split(const KArgs& a, hipStream_t st);
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st);
 
 }  // namespace vsmp

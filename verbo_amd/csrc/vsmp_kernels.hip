@@ -2541,6 +2541,152 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   }
 }
 
+// ---- split greedy rows: a small greedy batch, each row cut into parts over several CUs ----------
+//
+// With fewer rows than CUs, one workgroup per row leaves most of the chip idle. Here row r's 16-byte
+// groups are cut into P contiguous parts, one workgroup each, all in one launch. A part takes the
+// largest composite of its penalised values (src/sampler.cpp:53-70: the first maximum) and folds it
+// into the row's slot with a device-scope atomic max; the part that arrives last (a device-scope
+// ticket) takes the slot, writes the id and clears slot and ticket for the next call. Every value
+// that crosses workgroups travels in a device-scope atomic, and each part's atomics have completed
+// (vmcnt(0)) before its ticket is taken, so the last part's exchange sees every part's maximum. (A
+// release / acquire pair instead writes back and invalidates the XCD's L2 in every part: measured
+// 2x slower.)
+
+constexpr int kSplitNT = 512;
+constexpr int kSplitU = 8;                             // 16-byte loads per thread, all in flight at once
+constexpr int kSplitMaxGroups = kSplitNT * kSplitU;    // groups per part (64 KB)
+static_assert(kSplitMaxGroups == kSplitMaxPartGroups, "the planner sizes parts by kSplitMaxPartGroups");
+
+// One part's first maximum (composite key; 0 for an empty part). PEN: the history window has ids
+// to penalise. Every load is unconditional within an instance (an empty part rereads the row's last
+// group), so that each wait covers exactly the loads it needs.
+template <bool PEN>
+__device__ __forceinline__ uint64_t greedy_part(const KArgs& a, int row, int g0, int g1, int hfrom, int h1,
+                                                uint32_t* bits, uint64_t* red64) {
+  const int tid = threadIdx.x;
+  const int V = a.V;
+  const int V4 = (V + 3) >> 2;
+  const int lo = 4 * g0;  // the part's elements: [lo, hi)
+  const int hi = min(V, 4 * g1);
+  const float rep = a.shared.repeat;
+  // history ids first (the vector memory counter retires in order), then every load of the part
+  constexpr int HQ = 4;
+  int hid[HQ];
+  if (PEN) {
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) hid[q] = a.hist[min(hfrom + q * kSplitNT + tid, h1 - 1)];
+  }
+  const uint4* rp4 = reinterpret_cast<const uint4*>(a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld));
+  const int glast = g1 > g0 ? g1 - 1 : V4 - 1;
+  uint4 v[kSplitU];
+#pragma unroll
+  for (int u = 0; u < kSplitU; ++u) v[u] = stream_ld(rp4 + min(g0 + u * kSplitNT + tid, glast));
+
+  // penalty bitmap of the part (src/sampler.cpp:53-65)
+  const int words = (hi - lo + 31) >> 5;
+  if (PEN) {
+    for (int i = tid; i < words; i += kSplitNT) bits[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) {
+      const int id = hid[q];
+      if (hfrom + q * kSplitNT + tid < h1 && id >= lo && id < hi) atomicOr(&bits[(id - lo) >> 5], 1u << ((id - lo) & 31));
+    }
+    for (int i = hfrom + HQ * kSplitNT + tid; i < h1; i += kSplitNT) {
+      const int id = a.hist[i];
+      if (id >= lo && id < hi) atomicOr(&bits[(id - lo) >> 5], 1u << ((id - lo) & 31));
+    }
+    __syncthreads();
+  }
+
+  // per thread in increasing index order (strictly larger keys only: the first maximum stays)
+  uint32_t bk = 0u;
+  int bi = 0;
+#pragma unroll
+  for (int u = 0; u < kSplitU; ++u) {
+    const int f = g0 + u * kSplitNT + tid;
+    if (f >= g1) continue;
+    const int e = 4 * f;
+    float x[4] = {__uint_as_float(v[u].x), __uint_as_float(v[u].y), __uint_as_float(v[u].z), __uint_as_float(v[u].w)};
+    if (PEN) {
+      const uint32_t nib = (bits[(e - lo) >> 5] >> ((e - lo) & 31)) & 0xFu;
+      if (nib) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (nib & (1u << c)) x[c] = penalise(x[c], rep);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t k = e + c < V ? ord_key(x[c]) : 0u;
+      if (k > bk) {
+        bk = k;
+        bi = e + c;
+      }
+    }
+  }
+  return block_max64<kSplitNT>(bk ? comp(bk, static_cast<uint32_t>(bi)) : 0ull, red64);
+}
+
+__global__ __launch_bounds__(kSplitNT) void k_greedy_split(KArgs a) {
+  __shared__ uint32_t bits[kSplitMaxGroups / 8];  // the part's penalty bitmap (4 elements per group)
+  __shared__ uint64_t red64[kSplitNT / 64];
+  __shared__ uint32_t red32[kSplitNT / 64];
+  const int row = static_cast<int>(blockIdx.x) / a.P;
+  const int part = static_cast<int>(blockIdx.x) - row * a.P;
+  const int tid = threadIdx.x;
+  const vsmp_params& P = a.shared;
+  const int V = a.V;
+  const int V4 = (V + 3) >> 2;
+  const int G = (V4 + a.P - 1) / a.P;
+  const int g0 = min(V4, part * G), g1 = min(V4, g0 + G);
+  int h0 = 0, h1 = 0;
+  if (a.hist_off) {
+    h0 = a.hist_off[row];
+    h1 = a.hist_off[row + 1];
+  }
+  const int H = h1 - h0;
+  const bool pen = (P.repeat != 1.0f) && H > 0;
+  const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
+  const uint64_t best = pen ? greedy_part<true>(a, row, g0, g1, hfrom, h1, bits, red64)
+                            : greedy_part<false>(a, row, g0, g1, hfrom, h1, bits, red64);
+  const int lo = 4 * g0;
+  const int hi = min(V, 4 * g1);
+  const int words = (hi - lo + 31) >> 5;
+  uint32_t np = 0;
+  if (a.info && pen) {
+    for (int i = tid; i < words; i += kSplitNT) np += __popc(bits[i]);
+    np = block_sum_u32<kSplitNT>(np, red32);
+  }
+  if (tid == 0) {
+    __hip_atomic_fetch_max(&a.g_slot[row], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.info) __hip_atomic_fetch_add(&a.g_npen[row], np, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this part's atomics have completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const unsigned t = __hip_atomic_fetch_add(&a.g_tick[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == static_cast<unsigned>(a.P - 1)) {  // the last part: every part's maximum is in the slot
+      const uint64_t b = __hip_atomic_exchange(&a.g_slot[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t npr = a.info ? __hip_atomic_exchange(&a.g_npen[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+      __hip_atomic_store(&a.g_tick[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int id = comp_idx(b);
+      a.out[row] = id;
+      if (a.info) {
+        vsmp_row_info inf = {};
+        inf.id = id;
+        inf.path = kPathGreedy;
+        inf.k = inf.keep_minp = inf.keep = 1;
+        inf.rank = 0;
+        inf.last_id = id;
+        inf.mx = comp_val(b);
+        inf.n_pen = static_cast<int>(npr);
+        a.info[row] = inf;
+      }
+    }
+  }
+}
+
 // ---- read probe: a plain grid-stride streaming read (diagnostics) ----------------------------
 
 __global__ __launch_bounds__(256) void k_read_probe(const uint4* __restrict__ p, long long n16, unsigned* sink) {
@@ -2566,6 +2712,10 @@ __global__ __launch_bounds__(256) void k_exp_probe(const double* __restrict__ x,
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st) {
   const long long blocks = std::min<long long>((n + 255) / 256, 4096);
   hipLaunchKernelGGL(k_exp_probe, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, x, y, n);
+}
+
+void launch_greedy_split(const KArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_greedy_split, dim3(static_cast<unsigned>(a.B * a.P)), dim3(kSplitNT), 0, st, a);
 }
 
 void launch_read_probe(const void* p, long long n16, unsigned* sink, int grid, hipStream_t st) {
