@@ -342,3 +342,29 @@ def test_greedy_split_parts(ctx, monkeypatch, dmode):
     out = ctx.pick_batch(d, pr, torch.from_numpy(h).cuda(), torch.from_numpy(off).cuda())
     torch.cuda.synchronize()
     assert (out.cpu().numpy() == run.o_ids).all()
+
+
+def test_vocabulary_beyond_the_row_kernel(ctx):
+    """V above 2^19, where the planner's default is slices: shared and per-row parameters (small-k,
+    general and greedy rows), a history, ties at the maximum, against the oracle."""
+    rng = np.random.default_rng(41)
+    Vv = 600_003
+    B = 4
+    lg = rng.normal(0, 2, (B, Vv)).astype(np.float32)
+    lg[:, rng.choice(Vv, 5, replace=False)] = lg.max() + 1.0
+    hists = [list(rng.integers(-3, Vv + 3, 200)) for _ in range(B)]
+    h, off = csr(hists)
+    for p in (V.params_array(n=1, temp=0.8, top_k=50, top_p=0.95, min_p=0.05, repeat=1.1, repeat_last=0, seed=3),
+              V.params_array(n=1, temp=0.0, repeat=1.1, repeat_last=64, seed=3)):
+        log("large V shared", Vv, p["temp"][0])
+        Run(ctx, lg, p, h, off, cand_cap=64).report()
+    p = np.zeros(B, V.SAMPLING_DTYPE)
+    p["temp"] = [0.0, 0.7, 1.0, 1.3]
+    p["top_k"] = [40, 40, 0, 1000]
+    p["top_p"] = [0.9, 0.9, 0.99, 0.5]
+    p["min_p"] = [0.0, 0.02, 0.0, 0.0]
+    p["repeat"] = [1.2, 1.2, 1.0, 0.9]
+    p["repeat_last"] = [0, 16, 64, 0]
+    p["seed"] = [11, 12, 13, 14]
+    log("large V per row", Vv)
+    Run(ctx, lg, p, h, off, cand_cap=64).report()
