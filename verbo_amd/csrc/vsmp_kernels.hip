@@ -356,6 +356,18 @@ __device__ __forceinline__ double dpp_f64(double v) {
   return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<uint32_t>(lo));
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts, then row broadcasts).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  int x = static_cast<int>(v);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
+  return static_cast<uint32_t>(x);
+}
+
 // Inclusive prefix sum of doubles over the 64 lanes of a wave (a tree order, not the sequential one).
 __device__ __forceinline__ double wave_incl_scan_f64(double v) {
   v += dpp_f64<0x111, 0xf>(v);
@@ -1020,45 +1032,47 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
 
   // small k: sort the union of the slice lists (at most kMergeCap entries), keep the first k
   const int k = top_k_of(P, V);
-  if (tid == 0) {
-    int off = 0, fl = 0, np = 0;
-    for (int s = 0; s < S; ++s) {
-      const int c = a.s_cnt[row * S + s];
-      fl |= c >> 30;
-      sm_off[s] = off;
-      off += c & 0x3FFFFFFF;
-      np += a.s_npen[row * S + s];
+  // Each slice list is sorted, so with m = ceil(k / S) the smallest m-th entry over the lists that
+  // hold m bounds the row's k-th composite from below whenever those lists hold k entries in all:
+  // only entries at or above it can be in the top k. Wave 0 reads the S <= 64 slice counts and
+  // m-th entries in parallel (one lane each) and scans the offsets.
+  const int m = (k + S - 1) / S;
+  if (tid < 64) {
+    int c = 0, np = 0;
+    uint64_t mth = ~0ull;
+    if (tid < S) {
+      c = a.s_cnt[row * S + tid];
+      np = a.s_npen[row * S + tid];
     }
-    sm_off[S] = off;
-    sm_int[5] = fl ? VSMP_FLAG_FALLBACK : 0;
-    sm_int[6] = np;
+    const int len = c & 0x3FFFFFFF;
+    if (tid < S && len >= m) mth = a.s_cand[static_cast<size_t>(row * S + tid) * kKmax + (m - 1)];
+    const uint32_t incl = wave_incl_scan(static_cast<uint32_t>(len));
+    if (tid < S) sm_off[tid] = static_cast<int>(incl) - len;
+    if (tid == S - 1) sm_off[S] = static_cast<int>(incl);
+    const uint64_t fl = __ballot(tid < S && (c >> 30) != 0);
+    const uint64_t full = __ballot(tid < S && len >= m);
+    for (int o = 32; o > 0; o >>= 1) {
+      np += __shfl_xor(np, o);
+      mth = min64(mth, __shfl_xor(mth, o));
+    }
+    if (tid == 0) {
+      sm_int[5] = fl ? VSMP_FLAG_FALLBACK : 0;
+      sm_int[6] = np;
+      sm_int[7] = 0;
+      sm_red64[0] = static_cast<long long>(__popcll(full)) * m >= k ? mth : 0ull;
+    }
   }
   __syncthreads();
   const int M = sm_off[S];
-  // Each slice list is sorted, so with m = ceil(k / S) the smallest m-th entry over the lists that
-  // hold m bounds the row's k-th composite from below whenever those lists hold k entries in all:
-  // only entries at or above it can be in the top k.
-  uint64_t lb = 0ull;
-  {
-    const int m = (k + S - 1) / S;
-    int full = 0;
-    uint64_t mn = ~0ull;
-    for (int s2 = 0; s2 < S; ++s2) {
-      const int len = sm_off[s2 + 1] - sm_off[s2];
-      if (len >= m) {
-        ++full;
-        mn = min64(mn, a.s_cand[static_cast<size_t>(row * S + s2) * kKmax + (m - 1)]);
-      }
-    }
-    if (static_cast<long long>(full) * m >= k) lb = mn;
-  }
-  if (tid == 0) sm_int[7] = 0;
+  const uint64_t lb = sm_red64[0];
   __syncthreads();
-  for (int i = tid; i < M; i += kTpb) {
-    int s2 = 0;
-    while (sm_off[s2 + 1] <= i) ++s2;
-    const uint64_t v = a.s_cand[static_cast<size_t>(row * S + s2) * kKmax + (i - sm_off[s2])];
-    if (v >= lb) sm_buf[atomicAdd(&sm_int[7], 1)] = v;
+  // the entries >= lb, one wave per slice list
+  for (int s2 = tid >> 6; s2 < S; s2 += kTpb / 64) {
+    const int len = sm_off[s2 + 1] - sm_off[s2];
+    for (int i = tid & 63; i < len; i += 64) {
+      const uint64_t v = a.s_cand[static_cast<size_t>(row * S + s2) * kKmax + i];
+      if (v >= lb) sm_buf[atomicAdd(&sm_int[7], 1)] = v;
+    }
   }
   __syncthreads();
   const int C = sm_int[7];  // >= k
@@ -1952,17 +1966,6 @@ __device__ __forceinline__ uint32_t key_of(uint32_t bits) {
 
 __device__ __forceinline__ bool bit_of(const uint32_t* bits, int e) { return (bits[e >> 5] >> (e & 31)) & 1u; }
 
-// Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts, then row broadcasts).
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
-  int x = static_cast<int>(v);
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
-  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
-  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
-  return static_cast<uint32_t>(x);
-}
 
 // Maximum over the 64 lanes of a wave (DPP row shifts and broadcasts; lane 63 collects it).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
