@@ -368,3 +368,59 @@ def test_vocabulary_beyond_the_row_kernel(ctx):
     p["seed"] = [11, 12, 13, 14]
     log("large V per row", Vv)
     Run(ctx, lg, p, h, off, cand_cap=64).report()
+
+
+def test_graph_capture_and_replay(ctx):
+    """vsmp_pick_batch captured into a HIP graph (after one eager call has sized the scratch) and
+    replayed with new logits and draws copied into the captured buffers between replays: every
+    replay equals the eager call on the same inputs, for a greedy batch (split mode), a top-k batch
+    (row mode) and a general batch (row mode + k_general), all three in one graph."""
+    import torch
+
+    rng = np.random.default_rng(51)
+    B, Vv = 8, 30000
+    cases = [V.params_array(n=1, temp=0.0, repeat=1.2, repeat_last=0, seed=1),
+             V.params_array(n=1, temp=0.8, top_k=40, top_p=0.9, min_p=0.02, repeat=1.1, repeat_last=0, seed=1),
+             V.params_array(n=1, temp=1.0, top_k=0, top_p=0.95, repeat=1.1, repeat_last=0, seed=1)]
+    prm = [V.Params(*[p[0][f].item() for f in V.SAMPLING_DTYPE.names]) for p in cases]
+    h, off = csr([list(rng.integers(0, Vv, 100)) for _ in range(B)])
+    dh, doff = torch.from_numpy(h).cuda(), torch.from_numpy(off).cuda()
+    lg = torch.zeros((B, Vv), dtype=torch.float32, device="cuda")
+    u = torch.zeros(B, dtype=torch.float64, device="cuda")
+    outs = [torch.zeros(B, dtype=torch.int32, device="cuda") for _ in cases]
+
+    def fill(seed):
+        r = np.random.default_rng(seed)
+        lg.copy_(torch.from_numpy(r.normal(0, 2, (B, Vv)).astype(np.float32)))
+        u.copy_(torch.from_numpy(r.random(B)))
+
+    def eager():
+        res = []
+        for p in prm:
+            res.append(ctx.pick_batch(lg, p, dh, doff, V.U_SUPPLIED, u).cpu().numpy())
+        return res
+
+    fill(0)
+    eager()  # sizes the scratch outside the capture
+    torch.cuda.synchronize()
+    st = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            for p, o in zip(prm, outs):
+                ctx.pick_batch(lg, p, dh, doff, V.U_SUPPLIED, u, out=o, stream=st)
+    torch.cuda.synchronize()
+    for rep in range(5):
+        fill(100 + rep)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = [o.cpu().numpy() for o in outs]
+        want = eager()
+        torch.cuda.synchronize()
+        log("graph replay", rep)
+        for c in range(len(cases)):
+            assert (got[c] == want[c]).all(), (rep, c, got[c], want[c])
+        lgn = lg.cpu().numpy()
+        o_ids = O.pick_rows(lgn, cases[0], h, off, u.cpu().numpy())[0]
+        assert (got[0] == o_ids).all()
