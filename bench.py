@@ -11,7 +11,8 @@ replicated into enough buffers (> 600 MB) that consecutive steps never find thei
 Fields: value = rows/s over the timed steps; roofline.achieved = algorithmic bytes per call /
 mean call duration (two HIP events around the timed steps, on the launch stream); cpu_baseline = the reference sampler
 compiled from its sources (oracle/_ref), or the oracle restatement when that is not built, timed
-on this host for a bounded sample of the same rows.
+on this host for a bounded sample of the same rows: one thread (value, cores) and every host
+thread (value_all_cores, cores_all).
 """
 import argparse
 import json
@@ -39,9 +40,22 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def host_threads():
+    """CPU threads this process may use: its affinity set, capped by OMP_NUM_THREADS when set."""
+    import os
+
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
 def cpu_baseline(w, budget):
-    """Time the reference sampler's pick() on this host (1 thread) for `budget` seconds over the
-    workload's rows. Uses oracle/_ref when built, else the oracle restatement."""
+    """Time the reference sampler's pick() on this host over the workload's rows: one thread for
+    `budget` seconds (the reported value), then every host thread (rows statically partitioned, one
+    sampler per row) for half of it. Uses oracle/_ref when built, else the oracle restatement (one
+    thread only)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import numpy as np
 
@@ -50,8 +64,12 @@ def cpu_baseline(w, budget):
     params = w.params.copy()
     params["repeat_last"] = 0
     kind = "reference" if O.ref_available() else "port"
+    res = {}
     if kind == "reference":
         secs, picks = O.ref_time_rows(w.logits, params, w.hist, w.hist_off, threads=1, budget_s=budget)
+        nt = min(host_threads(), w.B)
+        secs_all, picks_all = O.ref_time_rows(w.logits, params, w.hist, w.hist_off, threads=nt, budget_s=budget / 2)
+        res = {"value_all_cores": picks_all / secs_all, "cores_all": nt}
     else:
         lib = O.load_oracle()
         u = np.full(w.B, 0.5)
@@ -61,9 +79,11 @@ def cpu_baseline(w, budget):
             picks += w.B
         secs = time.perf_counter() - t0
         del lib
-    return {"value": picks / secs, "unit": "rows/s", "cores": 1, "kind": kind,
-            "sample": f"{picks} pick() calls cycling over the {w.B} rows of the same workload for {secs:.1f} s, "
-                      f"1 thread, pick only (history accepted beforehand)"}
+    out = {"value": picks / secs, "unit": "rows/s", "cores": 1, "kind": kind,
+           "sample": f"{picks} pick() calls cycling over the {w.B} rows of the same workload for {secs:.1f} s, "
+                     f"1 thread, pick only (history accepted beforehand)"}
+    out.update(res)
+    return out
 
 
 def traffic_from_profiles(name):
