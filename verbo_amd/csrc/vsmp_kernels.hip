@@ -1136,9 +1136,8 @@ __device__ __forceinline__ uint32_t* gen_lds_bits() {
 // loads in flight (a and b); every load is issued unconditionally (past the row it rereads the last
 // 16-byte group, which 4*ceil(V/4) <= ld keeps inside the row), so each wait covers exactly the
 // buffer about to be processed.
-template <class F, class F4, class W>
+template <int U, class F, class F4, class W>
 __device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, F4&& f4, W&& word) {
-  constexpr int U = 1;
   constexpr int step = kGenThreads * 4 * U;
   const int tid = static_cast<int>(threadIdx.x);
   const float4* rp4 = reinterpret_cast<const float4*>(R.rp);
@@ -1185,17 +1184,19 @@ __device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, F4&& f4, W
 // Two loops rather than one with a chosen pointer: a pointer that may be LDS or global memory
 // becomes a flat load, which waits on the vector memory counter as well.
 // f(index, value) is called per element; f4(index of the first, values[4]) for each whole
-// 16-byte group, which lets a caller order the work of four elements itself.
-template <class F, class F4>
+// 16-byte group, which lets a caller order the work of four elements itself. U: 16-byte loads per
+// thread and buffer (two buffers in flight); U = 4 for the select passes measured slower (the
+// kernel's code grows by half and every phase slows), so every pass takes U = 1.
+template <int U, class F, class F4>
 __device__ __forceinline__ void gen_pass_groups(const GenRow& R, F&& f, F4&& f4) {
   if (R.lds_bits)
-    gen_pass_loop(R, f, f4, [](int i) { return gen_lds_bits()[i]; });
+    gen_pass_loop<U>(R, f, f4, [](int i) { return gen_lds_bits()[i]; });
   else
-    gen_pass_loop(R, f, f4, [&R](int i) { return R.bits[i]; });
+    gen_pass_loop<U>(R, f, f4, [&R](int i) { return R.bits[i]; });
 }
-template <class F>
+template <int U = 1, class F>
 __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
-  gen_pass_groups(R, f, [&f](int e, const float (&x)[4]) {
+  gen_pass_groups<U>(R, f, [&f](int e, const float (&x)[4]) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) f(e + c, x[c]);
   });
@@ -1607,7 +1608,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
         atomicAdd(&sh.mass0[q], p);
       }
     };
-    gen_pass_groups(
+    gen_pass_groups<1>(
         g.R,
         [&](int e, float v) {
           if (!excluded(e, v)) add(v, numer_g(g, v));
@@ -1831,7 +1832,8 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       const int ra_p = qp > 0 ? static_cast<int>(sh.cnt0[qp - 1]) : 0;
       const int n_p = static_cast<int>(sh.cnt0[qp]) - ra_p;
       const double above_p = qp > 0 ? sh.mass0[qp - 1] : 0.0;
-      if (static_cast<int>(sh.cnt0[qp]) < keep && n_p <= kGenCap / 2 && u * above_p > 0.0) {
+      // (qp = 0, the cut inside the maximum's bucket, gives d_lo = 0: bucket 0 holds the maximum)
+      if (static_cast<int>(sh.cnt0[qp]) < keep && n_p <= kGenCap / 2) {
         const int d_lo = find_bucket(u * above_p);
         const int d_hi = find_bucket(u * sh.mass0[qp] * (1.0 + 1e-12));  // slack: tot's sum order differs
         const int base_d = d_lo > 0 ? static_cast<int>(sh.cnt0[d_lo - 1]) : 0;
@@ -1881,7 +1883,11 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       }
     }
   }
-  if (!shared && topp) apply_topp(mass_select(tp * sum));
+  // src/sampler.cpp:92-100 can only shorten the kept set when that set holds top_p of the mass: a
+  // min-p prefix whose mass is clearly below top_p * sum (relative margin 1e-12, far above the
+  // rounding of either sum) is kept whole, and its top-p select pass is not needed
+  const bool topp_may_cut = !(tot < tp * sum * (1.0 - 1e-12));
+  if (!shared && topp && topp_may_cut) apply_topp(mass_select(tp * sum));
   if (!drawn) {
     target = u * tot;
     d = mass_select(target);
