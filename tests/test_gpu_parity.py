@@ -258,6 +258,11 @@ def _general_batch(rng, kind, B=24, Vv=30000):
         p["min_p"] = rng.choice([0.05, 0.1], B)
         p["repeat"] = 1.2
         hists = [rng.integers(0, Vv, int(rng.integers(0, 200))) for _ in range(B)]
+    elif kind == "minp_large":  # min-p prefixes of thousands: top-p may cut inside them, or cannot
+        lg = rng.normal(0, 0.5, (B, Vv))
+        p["temp"] = 0.25
+        p["min_p"] = rng.choice([0.005, 0.008, 0.012], B)
+        p["top_p"] = np.where(np.arange(B) % 2 == 0, 0.3, 0.995)
     elif kind == "cold":  # the buckets stop far short of the minimum: the overflow bucket holds most rows
         lg = rng.normal(0, 2.0, (B, Vv))
         p["temp"] = rng.choice([0.005, 0.02, 0.05], B)
@@ -274,9 +279,9 @@ def _general_batch(rng, kind, B=24, Vv=30000):
     return lg.astype(np.float32), p, h, off
 
 
-@pytest.mark.parametrize("kind", ["flat", "minp", "cold", "interleaved"])
+@pytest.mark.parametrize("kind", ["flat", "minp", "minp_large", "cold", "interleaved"])
 def test_general_path_pass_plans(ctx, mode, kind):
-    rng = np.random.default_rng({"flat": 11, "minp": 12, "cold": 13, "interleaved": 14}[kind])
+    rng = np.random.default_rng({"flat": 11, "minp": 12, "minp_large": 15, "cold": 13, "interleaved": 14}[kind])
     lg, p, h, off = _general_batch(rng, kind)
     log("general pass plan", mode, kind)
     run = Run(ctx, lg, p, h, off)
@@ -287,6 +292,10 @@ def test_general_path_pass_plans(ctx, mode, kind):
         assert (flags & V.FLAG_ONE_PASS).mean() >= 0.5, flags
     if kind == "minp":
         assert (flags & V.FLAG_MINP_PREFIX).mean() >= 0.5, flags
+    if kind == "minp_large":  # prefixes beyond the whole-prefix collection, both top-p outcomes
+        keep_m, keep = run.info["keep_minp"][gen], run.info["keep"][gen]
+        big = keep_m > 1024
+        assert (big & (keep < keep_m)).any() and (big & (keep == keep_m)).any(), (keep_m, keep)
     if kind == "interleaved":
         assert gen.any() and (~gen).any()
 
