@@ -7,17 +7,20 @@
 //
 // Kernels, stream-ordered (each kernel boundary publishes the previous one's results; no
 // workgroup waits on another):
-//  k_rows    one 1024-thread workgroup per row, for batches with at least one row per CU: streams
-//            the row once (penalty from an LDS bitmap of the history window), keeps only elements
-//            above a row bound taken from its first chunks, selects the exact top-k and runs the
-//            reference's epilogue (softmax numerators, min-p, top-p, draw).
-//  k_stage1  smaller batches, grid = rows x slices. Each workgroup loads one slice of one row into
-//            registers (the single HBM pass), applies the penalty and writes its slice maximum;
-//            small-k rows (k <= 256) also write the slice's exact, sorted top-k.
-//  k_finish  one workgroup per greedy / small-k row: merges the slice results and runs the
-//            epilogue.
-//  k_general one workgroup per remaining row (k > 256 or top-k off): multi-pass radix select by
-//            count and by fp64 mass over the row, with histograms in LDS.
+//  k_rows    one 1024-thread workgroup per row whenever the row's history bitmap fits in LDS
+//            (V <= 2^19): streams the row once (penalty from an LDS bitmap of the history window),
+//            keeps only elements above a row bound taken from its first chunks, selects the exact
+//            top-k and runs the reference's epilogue (softmax numerators, min-p, top-p, draw).
+//  k_greedy_split  a greedy batch of at most half as many rows as CUs: each row cut into parts
+//            over several CUs; the part that takes the row's last device-scope ticket writes the
+//            id (every cross-workgroup value travels in a device-scope atomic).
+//  k_stage1  larger vocabularies (V > 2^19), grid = rows x slices. Each workgroup loads one slice
+//            of one row into registers (the single HBM pass), applies the penalty and writes its
+//            slice maximum; small-k rows (k <= 256) also write the slice's exact, sorted top-k.
+//  k_finish  one workgroup per greedy / small-k row after k_stage1: merges the slice results and
+//            runs the epilogue.
+//  k_general one workgroup per remaining row (k > 256 or top-k off): a mass histogram of the fp64
+//            numerators, then count and mass selects over the row, with histograms in LDS.
 //  k_read_probe  a plain streaming read, for the attainable-bandwidth measurement.
 //  k_exp_probe   the general path's fp64 exp over an array, for measuring its accuracy.
 #include <algorithm>
