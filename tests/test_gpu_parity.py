@@ -433,3 +433,50 @@ def test_graph_capture_and_replay(ctx):
         lgn = lg.cpu().numpy()
         o_ids = O.pick_rows(lgn, cases[0], h, off, u.cpu().numpy())[0]
         assert (got[0] == o_ids).all()
+
+
+@pytest.mark.parametrize("dmode", ["split", "rows"])
+def test_topk_split_parts(ctx, monkeypatch, dmode):
+    """Small-k batches cut into parts (one launch, the last part merges the parts' sorted lists and
+    runs the epilogue) against the oracle, and row mode on the same inputs: ties of the largest
+    values in different parts, penalised candidates, k from 1 to 256, min-p and top-p, parts that
+    end inside a 16-byte group or hold no group, all three draw modes (the xorshift state advanced
+    once per row), candidate lists, and consecutive calls reusing the per-row tickets."""
+    import torch
+
+    monkeypatch.setenv("VSMP_MODE", dmode)
+    rng = np.random.default_rng(61)
+    for B, Vv, k in [(1, 151936, 40), (3, 49152, 1), (2, 20001, 256), (8, 131075, 50), (5, 4097, 7),
+                     (1, 600_003, 100)]:
+        lg = rng.normal(0, 3, (B, Vv)).astype(np.float32)
+        for r in range(B):
+            lg[r, rng.choice(Vv, 6, replace=False)] = lg[r].max() + 0.5
+        hists = [list(rng.integers(-2, Vv + 2, int(rng.integers(0, 400)))) + [int(np.argmax(lg[r]))]
+                 for r in range(B)]
+        h, off = csr(hists)
+        p = V.params_array(n=1, temp=0.9, top_k=k, top_p=0.9, min_p=0.02, repeat=1.2, repeat_last=0, seed=9)
+        log("topk split", dmode, B, Vv, k)
+        run = Run(ctx, lg, p, h, off, cand_cap=64)
+        run.report()
+        assert (run.info["path"] == V.PATH_SMALLK).all()
+    # the reference's own draw stream, shared parameters: each row's state advances once per pick
+    B, Vv = 4, 151936
+    lg = rng.normal(0, 3, (B, Vv)).astype(np.float32)
+    p = V.params_array(n=1, temp=0.8, top_k=40, top_p=0.95, repeat=1.0, repeat_last=0, seed=9)
+    st = np.zeros((B, 2), np.uint64)
+    for r in range(B):
+        s0 = O.rng_seed(1000 + r)
+        st[r] = [s0[0], s0[1]]
+    dst = torch.from_numpy(st.view(np.int64).copy()).cuda()
+    d = torch.from_numpy(lg).cuda()
+    pr = V.Params(*[p[0][f].item() for f in V.SAMPLING_DTYPE.names])
+    for step in range(3):
+        log("topk split xorshift", dmode, step)
+        ids = ctx.pick_batch(d, pr, u_mode=V.U_XORSHIFT, rng_state=dst).cpu().numpy()
+        u = np.zeros(B)
+        for r in range(B):
+            s1 = (O.ctypes.c_uint64 * 2)(int(st[r, 0]), int(st[r, 1]))
+            u[r] = O.rng_unit(s1)
+            st[r] = [s1[0], s1[1]]
+        assert (ids == O.pick_rows(lg, p, u=u)[0]).all()
+        assert (dst.cpu().numpy().view(np.uint64) == st).all()

@@ -109,16 +109,18 @@ namespace {
 
 struct Plan {
   bool rows;   // row mode: one workgroup per row (k_rows), else slices (k_stage1 + k_finish)
-  bool split;  // a small greedy batch: each row cut into P parts in one launch (k_greedy_split)
+  bool split;  // a small greedy or top-k batch: each row cut into P parts in one launch
+  bool topk;   // ... of small-k rows (k_topk_split), else greedy rows (k_greedy_split)
   int P;
   int ept, S, L, grid, xcd, smallk_ok;
   bool any_general, any_smallk, any_finish;
 };
 
 // VSMP_MODE=rows|slices|split pins the decomposition (testing and tuning); default: split parts
-// for a greedy batch of at most half as many rows as CUs, else rows whenever the vocabulary fits
-// the row kernel (V <= 2^19), slices beyond. split applies to greedy batches with shared
-// parameters only; other batches take the default.
+// for a greedy batch of at most half as many rows as CUs, or a small-k batch of at most 8 long rows
+// (topk_parts), else rows whenever the vocabulary fits the row kernel (V <= 2^19), slices beyond.
+// split applies to greedy and small-k batches with shared parameters only; other batches take the
+// default.
 int forced_mode() {
   const char* e = std::getenv("VSMP_MODE");
   if (!e) return -1;
@@ -147,19 +149,47 @@ int split_parts(int B, int V, int cus, bool forced) {
   return static_cast<int>(std::max<long long>(P, 1));
 }
 
+// Parts per row of a split small-k batch: the fewest parts of at most kSplitMaxPartGroups groups
+// (a part's cost is mostly fixed, and the last part merges one list per part), within what the last
+// part can merge (at most kMaxMergeSlices lists, P * k <= kMergeCap entries). 0: no split.
+int topk_parts(int B, int V, int cus, int k, bool forced) {
+  const long long V4 = (static_cast<long long>(V) + 3) / 4;
+  const long long pmin = (V4 + kSplitMaxPartGroups - 1) / kSplitMaxPartGroups;
+  const long long kk = std::max(1, std::min(k, kKmax));
+  const long long pmax = std::min<long long>({std::max(pmin, V4 / 512), kMaxMergeSlices, kMergeCap / kk});
+  if (pmin > pmax) return 0;
+  static const long long forced_p = [] {
+    const char* e = std::getenv("VSMP_SPLIT_P");
+    return e ? std::atoll(e) : 0LL;
+  }();
+  const long long P = forced_p > 0 ? std::min(std::max(forced_p, pmin), pmax) : pmin;
+  // Measured against row mode (top-k 40, V = 151936): faster at B = 1 and 8 (18.8 / 20.4 against
+  // 21.5 / 22.8 us), even at 16, slower from 32 on; slower at any B when the row is short (one
+  // workgroup streams it quickly: V = 49152, 17.8 against 14.0 us). Default: B <= 8, P >= 8.
+  if (!forced && (B > 8 || P < 8)) return 0;
+  if (static_cast<long long>(B) * P > INT32_MAX) return 0;
+  return static_cast<int>(std::max<long long>(P, 1));
+}
+
 // Slice shape: enough workgroups to fill the chip (>= 2048), slices of 256*EPT elements, and no
 // more slices than the small-k merge can hold (S * k <= kMergeCap).
 Plan plan(int B, int V, const vsmp_params* hostp, int cus) {
   Plan pl{};
   const int fm = forced_mode();
-  if (hostp && path_host(*hostp, V, true) == kPathGreedy && (fm == -1 || fm == 2)) {
-    const int P = split_parts(B, V, cus, fm == 2);
+  if (hostp && (fm == -1 || fm == 2)) {
+    const int path = path_host(*hostp, V, true);
+    const int k = (hostp->top_k > 0 && hostp->top_k < V) ? hostp->top_k : V;
+    const int P = path == kPathGreedy ? split_parts(B, V, cus, fm == 2)
+                                      : (path == kPathSmallK ? topk_parts(B, V, cus, k, fm == 2) : 0);
     if (P > 0) {
       pl.split = true;
+      pl.topk = path == kPathSmallK;
       pl.P = P;
-      pl.S = 1;
+      pl.S = P;  // the slice scratch holds one list per part
       pl.L = V;
       pl.grid = B * P;
+      pl.smallk_ok = 1;
+      pl.any_smallk = pl.topk;
       return pl;
     }
   }
@@ -295,7 +325,10 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
     a.g_slot = ctx->g_slot;
     a.g_tick = ctx->g_tick;
     a.g_npen = ctx->g_npen;
-    launch_greedy_split(a, st);
+    if (pl.topk)
+      launch_topk_split(a, st);
+    else
+      launch_greedy_split(a, st);
     return hip_ok(hipGetLastError(), "split launch") ? 0 : -1;
   }
   if (pl.rows) {

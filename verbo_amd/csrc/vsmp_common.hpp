@@ -71,6 +71,7 @@ void launch_rows(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
 void launch_read_probe(const void* p, long long n16, unsigned* sink, int grid, hipStream_t st);
 void launch_greedy_split(const KArgs& a, hipStream_t st);
+void launch_topk_split(const KArgs& a, hipStream_t st);
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st);
 
 }  // namespace vsmp

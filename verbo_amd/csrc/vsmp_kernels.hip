@@ -14,6 +14,8 @@
 //  k_greedy_split  a greedy batch of at most half as many rows as CUs: each row cut into parts
 //            over several CUs; the part that takes the row's last device-scope ticket writes the
 //            id (every cross-workgroup value travels in a device-scope atomic).
+//  k_topk_split  the same for a small-k batch of at most 8 long rows: each part selects its exact
+//            top-k; the last part merges the parts' lists and runs the epilogue.
 //  k_stage1  larger vocabularies (V > 2^19), grid = rows x slices. Each workgroup loads one slice
 //            of one row into registers (the single HBM pass), applies the penalty and writes its
 //            slice maximum; small-k rows (k <= 256) also write the slice's exact, sorted top-k.
@@ -991,6 +993,117 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
 // ---- finish: one workgroup per greedy / small-k row, after stage 1 -----------------------------
 // The kernel boundary orders stage 1's slice results before these reads.
 
+// The merge of a small-k row's slice (or part) lists and the reference epilogue, by one workgroup
+// of NT threads: S lists of at most kKmax sorted composites in s_cand, their counts in s_cnt
+// (bit 30: the slice used the exact fallback) and penalised-id counts in s_npen. COHERENT: the
+// lists were written in the same launch, by other workgroups, with device-scope stores, and are
+// read with device-scope loads; otherwise a kernel boundary has published them.
+template <int NT, bool COHERENT>
+__device__ void finish_smallk(const KArgs& a, int row, const vsmp_params& P, int S, uint64_t* sm_buf, uint64_t* sm_top,
+                              uint64_t* sm_red64, int* sm_int, int* sm_off) {
+  const int tid = threadIdx.x;
+  const int V = a.V;
+  auto ld = [](const auto* p) {
+    if (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+  };
+  // small k: sort the union of the slice lists (at most kMergeCap entries), keep the first k
+  const int k = top_k_of(P, V);
+  // Each slice list is sorted, so with m = ceil(k / S) the smallest m-th entry over the lists that
+  // hold m bounds the row's k-th composite from below whenever those lists hold k entries in all:
+  // only entries at or above it can be in the top k. Wave 0 reads the S <= 64 slice counts and
+  // m-th entries in parallel (one lane each) and scans the offsets.
+  const int m = (k + S - 1) / S;
+  if (tid < 64) {
+    int c = 0, np = 0;
+    uint64_t mth = ~0ull;
+    if (tid < S) {
+      c = ld(&a.s_cnt[row * S + tid]);
+      np = ld(&a.s_npen[row * S + tid]);
+    }
+    // the m-th entry is read along with the count (a list shorter than m leaves it unused)
+    uint64_t mt = ~0ull;
+    if (tid < S) mt = ld(&a.s_cand[static_cast<size_t>(row * S + tid) * kKmax + (m - 1)]);
+    const int len = c & 0x3FFFFFFF;
+    if (tid < S && len >= m) mth = mt;
+    const uint32_t incl = wave_incl_scan(static_cast<uint32_t>(len));
+    if (tid < S) sm_off[tid] = static_cast<int>(incl) - len;
+    if (tid == S - 1) sm_off[S] = static_cast<int>(incl);
+    const uint64_t fl = __ballot(tid < S && (c >> 30) != 0);
+    const uint64_t full = __ballot(tid < S && len >= m);
+    for (int o = 32; o > 0; o >>= 1) {
+      np += __shfl_xor(np, o);
+      mth = min64(mth, __shfl_xor(mth, o));
+    }
+    if (tid == 0) {
+      sm_int[5] = fl ? VSMP_FLAG_FALLBACK : 0;
+      sm_int[6] = np;
+      sm_int[7] = 0;
+      sm_red64[0] = static_cast<long long>(__popcll(full)) * m >= k ? mth : 0ull;
+    }
+  }
+  __syncthreads();
+  const int M = sm_off[S];
+  const uint64_t lb = sm_red64[0];
+  __syncthreads();
+  // the entries >= lb: entry i of the concatenated lists lies in list s2 with off[s2] <= i <
+  // off[s2 + 1] (binary search); eight loads per thread go out together
+  constexpr int PF = 8;
+  for (int i0 = 0; i0 < M; i0 += NT * PF) {
+    uint64_t vals[PF];
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = i0 + j * NT + tid;
+      vals[j] = 0ull;
+      if (i < M) {
+        int lo_ = 0, hi_ = S - 1;
+        while (lo_ < hi_) {
+          const int mid = (lo_ + hi_ + 1) >> 1;
+          if (sm_off[mid] <= i) lo_ = mid;
+          else hi_ = mid - 1;
+        }
+        vals[j] = ld(&a.s_cand[static_cast<size_t>(row * S + lo_) * kKmax + (i - sm_off[lo_])]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+      if (i0 + j * NT + tid < M && vals[j] >= lb) sm_buf[atomicAdd(&sm_int[7], 1)] = vals[j];
+  }
+  __syncthreads();
+  const int C = sm_int[7];  // >= k
+  if (C <= 2 * NT) {
+    // rank by counting (composites are distinct)
+    pad16(sm_buf, C, tid);
+    __syncthreads();
+    for (int i = tid; i < C; i += NT) {
+      const uint64_t x = sm_buf[i];
+      const int r = rank_count(sm_buf, C, x);
+      if (r < k) sm_top[r] = x;
+    }
+  } else {
+    int p2 = 1;
+    while (p2 < C) p2 <<= 1;
+    for (int i = C + tid; i < p2; i += NT) sm_buf[i] = 0ull;
+    bitonic_desc<NT>(sm_buf, p2);
+    for (int i = tid; i < k; i += NT) sm_top[i] = sm_buf[i];
+  }
+  __syncthreads();
+  if (tid < 64) {
+    double u = 0.0;
+    if (tid == 0) u = draw_u(a, row, P);
+    double* spr = reinterpret_cast<double*>(sm_buf) + kEpiWs;  // src/sampler.cpp:79-83
+    const float mx = comp_val(sm_top[0]);
+    for (int i = tid; i < k; i += 64) spr[i] = numer(comp_val(sm_top[i]), mx, P.temp);
+    wave_lds_sync();
+    if (k <= 64)
+      epilogue_wave<1>(a, row, P, sm_top, spr, k, sm_int[6], sm_int[5], readlane_f64(u, 0),
+                       reinterpret_cast<double*>(sm_buf));
+    else
+      epilogue_wave<kEpiJ>(a, row, P, sm_top, spr, k, sm_int[6], sm_int[5], readlane_f64(u, 0),
+                           reinterpret_cast<double*>(sm_buf));
+  }
+}
+
 __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
   __shared__ __align__(16) uint64_t sm_buf[kMergeCap];
   __shared__ uint64_t sm_top[kKmax];
@@ -1033,83 +1146,7 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
     return;
   }
 
-  // small k: sort the union of the slice lists (at most kMergeCap entries), keep the first k
-  const int k = top_k_of(P, V);
-  // Each slice list is sorted, so with m = ceil(k / S) the smallest m-th entry over the lists that
-  // hold m bounds the row's k-th composite from below whenever those lists hold k entries in all:
-  // only entries at or above it can be in the top k. Wave 0 reads the S <= 64 slice counts and
-  // m-th entries in parallel (one lane each) and scans the offsets.
-  const int m = (k + S - 1) / S;
-  if (tid < 64) {
-    int c = 0, np = 0;
-    uint64_t mth = ~0ull;
-    if (tid < S) {
-      c = a.s_cnt[row * S + tid];
-      np = a.s_npen[row * S + tid];
-    }
-    const int len = c & 0x3FFFFFFF;
-    if (tid < S && len >= m) mth = a.s_cand[static_cast<size_t>(row * S + tid) * kKmax + (m - 1)];
-    const uint32_t incl = wave_incl_scan(static_cast<uint32_t>(len));
-    if (tid < S) sm_off[tid] = static_cast<int>(incl) - len;
-    if (tid == S - 1) sm_off[S] = static_cast<int>(incl);
-    const uint64_t fl = __ballot(tid < S && (c >> 30) != 0);
-    const uint64_t full = __ballot(tid < S && len >= m);
-    for (int o = 32; o > 0; o >>= 1) {
-      np += __shfl_xor(np, o);
-      mth = min64(mth, __shfl_xor(mth, o));
-    }
-    if (tid == 0) {
-      sm_int[5] = fl ? VSMP_FLAG_FALLBACK : 0;
-      sm_int[6] = np;
-      sm_int[7] = 0;
-      sm_red64[0] = static_cast<long long>(__popcll(full)) * m >= k ? mth : 0ull;
-    }
-  }
-  __syncthreads();
-  const int M = sm_off[S];
-  const uint64_t lb = sm_red64[0];
-  __syncthreads();
-  // the entries >= lb, one wave per slice list
-  for (int s2 = tid >> 6; s2 < S; s2 += kTpb / 64) {
-    const int len = sm_off[s2 + 1] - sm_off[s2];
-    for (int i = tid & 63; i < len; i += 64) {
-      const uint64_t v = a.s_cand[static_cast<size_t>(row * S + s2) * kKmax + i];
-      if (v >= lb) sm_buf[atomicAdd(&sm_int[7], 1)] = v;
-    }
-  }
-  __syncthreads();
-  const int C = sm_int[7];  // >= k
-  if (C <= 2 * kTpb) {
-    // rank by counting (composites are distinct)
-    pad16(sm_buf, C, tid);
-    __syncthreads();
-    for (int i = tid; i < C; i += kTpb) {
-      const uint64_t x = sm_buf[i];
-      const int r = rank_count(sm_buf, C, x);
-      if (r < k) sm_top[r] = x;
-    }
-  } else {
-    int p2 = 1;
-    while (p2 < C) p2 <<= 1;
-    for (int i = C + tid; i < p2; i += kTpb) sm_buf[i] = 0ull;
-    bitonic_desc<kTpb>(sm_buf, p2);
-    for (int i = tid; i < k; i += kTpb) sm_top[i] = sm_buf[i];
-  }
-  __syncthreads();
-  if (tid < 64) {
-    double u = 0.0;
-    if (tid == 0) u = draw_u(a, row, P);
-    double* spr = reinterpret_cast<double*>(sm_buf) + kEpiWs;  // src/sampler.cpp:79-83
-    const float mx = comp_val(sm_top[0]);
-    for (int i = tid; i < k; i += 64) spr[i] = numer(comp_val(sm_top[i]), mx, P.temp);
-    wave_lds_sync();
-    if (k <= 64)
-      epilogue_wave<1>(a, row, P, sm_top, spr, k, sm_int[6], sm_int[5], readlane_f64(u, 0),
-                       reinterpret_cast<double*>(sm_buf));
-    else
-      epilogue_wave<kEpiJ>(a, row, P, sm_top, spr, k, sm_int[6], sm_int[5], readlane_f64(u, 0),
-                           reinterpret_cast<double*>(sm_buf));
-  }
+  finish_smallk<kTpb, false>(a, row, P, S, sm_buf, sm_top, sm_red64, sm_int, sm_off);
 }
 
 // ---- general path -------------------------------------------------------------------------------
@@ -2553,6 +2590,233 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   }
 }
 
+// ---- split top-k rows: a small batch of small-k rows, each row cut into parts in one launch -------
+//
+// The counterpart of k_greedy_split for rows with 0 < k <= 256 (src/sampler.cpp:71-108): row r's
+// 16-byte groups are cut into P contiguous parts, one 512-thread workgroup each. A part holds its
+// elements as penalised order keys in registers (all its loads in flight at once), bounds its
+// ks-th key from below by the ks-th largest of its 512 lane maxima (two 2048-bin histogram levels
+// in LDS), selects its exact top-ks composites among the keys above that bound with further
+// histogram passes over the registers, and writes them, sorted, with device-scope stores. The part
+// that takes the row's last device-scope ticket merges the P lists and runs the reference epilogue
+// (finish_smallk, as k_finish does after slices), then clears the ticket for the next call.
+
+constexpr int kTkNT = 512;
+constexpr int kTkW = kTkNT / 64;
+constexpr int kTkU = 8;                     // 16-byte loads per thread: the whole part in flight
+static_assert(kTkNT * kTkU == kSplitMaxPartGroups, "the planner sizes parts by kSplitMaxPartGroups");
+
+struct __align__(16) TkShared {
+  uint32_t bins[2][kRowBins];                // row-bound and select histograms (read as uint4)
+  uint32_t bits[kSplitMaxPartGroups / 8];    // the part's penalty bitmap (4 elements per group)
+  uint64_t top[kKmax];                       // the part's top-ks; the merged top-k
+  int rank[kKmax];
+  uint64_t red64[kTkW];
+  uint32_t red32[kTkW];
+  int ints[16];
+  int off[kMaxMergeSlices + 1];
+  uint64_t mbuf[kMergeCap];                  // the last part's merge and epilogue workspace
+};
+static_assert(kEpiWs + kKmax <= kMergeCap, "the epilogue's workspace and numerators live in mbuf");
+
+__global__ __launch_bounds__(kTkNT) void k_topk_split(KArgs a) {
+  __shared__ TkShared sh;
+  const int row = static_cast<int>(blockIdx.x) / a.P;
+  const int part = static_cast<int>(blockIdx.x) - row * a.P;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const vsmp_params& P = a.shared;
+  const int V = a.V;
+  const int V4 = (V + 3) >> 2;
+  const int G = (V4 + a.P - 1) / a.P;
+  const int g0 = min(V4, part * G), g1 = min(V4, g0 + G);
+  const int lo = 4 * g0;  // the part's elements: [lo, hi)
+  const int hi = min(V, 4 * g1);
+  const int ks = min(top_k_of(P, V), max(0, hi - lo));
+  const size_t slot = static_cast<size_t>(row) * a.P + part;
+
+  int h0 = 0, h1 = 0;
+  if (a.hist_off) {
+    h0 = a.hist_off[row];
+    h1 = a.hist_off[row + 1];
+  }
+  const int H = h1 - h0;
+  const bool pen = (P.repeat != 1.0f) && H > 0;
+  const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
+  constexpr int HQ = 4;
+  int hid[HQ];
+  if (pen) {
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) hid[q] = a.hist[min(hfrom + q * kTkNT + tid, h1 - 1)];
+  }
+  const uint4* rp4 = reinterpret_cast<const uint4*>(a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld));
+  const int glast = g1 > g0 ? g1 - 1 : V4 - 1;
+  uint4 v[kTkU];
+#pragma unroll
+  for (int u = 0; u < kTkU; ++u) v[u] = stream_ld(rp4 + min(g0 + u * kTkNT + tid, glast));
+
+  for (int i = tid; i < 2 * kRowBins; i += kTkNT) (&sh.bins[0][0])[i] = 0u;
+  if (tid == 0) sh.ints[8] = 0;
+  // penalty bitmap of the part (src/sampler.cpp:53-65)
+  const int words = (hi - lo + 31) >> 5;
+  if (pen) {
+    for (int i = tid; i < words; i += kTkNT) sh.bits[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) {
+      const int id = hid[q];
+      if (hfrom + q * kTkNT + tid < h1 && id >= lo && id < hi) atomicOr(&sh.bits[(id - lo) >> 5], 1u << ((id - lo) & 31));
+    }
+    for (int i = hfrom + HQ * kTkNT + tid; i < h1; i += kTkNT) {
+      const int id = a.hist[i];
+      if (id >= lo && id < hi) atomicOr(&sh.bits[(id - lo) >> 5], 1u << ((id - lo) & 31));
+    }
+  }
+  __syncthreads();
+
+  // penalised order keys in place (0: past the part), the lane maximum and the part's maximum
+  uint32_t lm = 0u;
+  uint64_t mxc = 0ull;
+#pragma unroll
+  for (int u = 0; u < kTkU; ++u) {
+    const int f = g0 + u * kTkNT + tid;
+    const int e = 4 * f;
+    float x[4] = {__uint_as_float(v[u].x), __uint_as_float(v[u].y), __uint_as_float(v[u].z), __uint_as_float(v[u].w)};
+    if (pen && f < g1) {
+      const uint32_t nib = (sh.bits[(e - lo) >> 5] >> ((e - lo) & 31)) & 0xFu;
+      if (nib) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (nib & (1u << c)) x[c] = penalise(x[c], P.repeat);
+      }
+    }
+    uint32_t kk[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      kk[c] = (f < g1 && e + c < V) ? ord_key(x[c]) : 0u;
+      lm = max(lm, kk[c]);
+      if (kk[c]) mxc = max64(mxc, comp(kk[c], static_cast<uint32_t>(e + c)));
+    }
+    v[u] = make_uint4(kk[0], kk[1], kk[2], kk[3]);
+  }
+  mxc = block_max64<kTkNT>(mxc, sh.red64);
+
+  // row bound T (to 2^10 keys): the ks-th largest lane maximum, from two histogram levels
+  uint32_t T = 0u;
+  if (ks > 0) {
+    atomicAdd(&sh.bins[0][lm >> 21], 1u);
+    __syncthreads();
+    if (w == 0) wave_find_bucket(sh.bins[0], ks, sh.ints);
+    __syncthreads();
+    const int b1 = sh.ints[0];
+    if (static_cast<int>(lm >> 21) == b1) atomicAdd(&sh.bins[1][(lm >> 10) & 2047u], 1u);
+    __syncthreads();
+    if (w == 0) wave_find_bucket(sh.bins[1], ks - sh.ints[1], sh.ints + 4);
+    __syncthreads();
+    const int b2 = sh.ints[4];
+    T = (b1 >= 0 && b2 >= 0) ? ((static_cast<uint32_t>(b1) << 21) | (static_cast<uint32_t>(b2) << 10)) : 0u;
+    T = __builtin_amdgcn_readfirstlane(T);
+    for (int i = tid; i < 2 * kRowBins; i += kTkNT) (&sh.bins[0][0])[i] = 0u;
+    __syncthreads();
+  }
+
+  // the exact ks-th largest composite: 2048-bin passes over the composites >= T << 32 in registers,
+  // each narrowing [lo, hi] to the bucket that holds it, until the bucket is taken whole
+  uint64_t clo = static_cast<uint64_t>(T) << 32, chi = mxc;
+  int need = ks;
+  for (int pass = 0; ks > 0 && clo != chi && pass < 9; ++pass) {
+    const uint64_t R = chi - clo;
+    const int sft = R < static_cast<uint64_t>(kRowBins) ? 0 : 53 - __clzll(static_cast<long long>(R));
+    uint32_t* bins = sh.bins[pass & 1];
+    for (int i = tid; i < kRowBins; i += kTkNT) sh.bins[(pass + 1) & 1][i] = 0u;
+#pragma unroll
+    for (int u = 0; u < kTkU; ++u) {
+      const uint32_t kk[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      const int e = 4 * (g0 + u * kTkNT + tid);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (kk[c] < T || kk[c] == 0u) continue;
+        const uint64_t cc = comp(kk[c], static_cast<uint32_t>(e + c));
+        if (cc >= clo && cc <= chi) atomicAdd(&bins[(cc - clo) >> sft], 1u);
+      }
+    }
+    __syncthreads();
+    if (w == 0) wave_find_bucket(bins, need, sh.ints);
+    __syncthreads();
+    const int b = sh.ints[0];
+    const int inb = sh.ints[2];
+    need -= sh.ints[1];
+    __syncthreads();
+    if (b < 0) break;  // unreachable: ks composites lie at or above T << 32
+    const uint64_t nlo = clo + (static_cast<uint64_t>(b) << sft);
+    const uint64_t wdt = sft == 0 ? 0ull : (1ull << sft) - 1ull;
+    chi = (chi - nlo < wdt) ? chi : nlo + wdt;
+    clo = nlo;
+    if (inb == need) chi = clo;  // the whole bucket is taken: the top ks are the composites >= clo
+  }
+
+  // collect the composites >= clo (exactly ks of them), rank them and store them sorted
+#pragma unroll
+  for (int u = 0; u < kTkU; ++u) {
+    const uint32_t kk[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+    const int e = 4 * (g0 + u * kTkNT + tid);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint64_t cc = kk[c] ? comp(kk[c], static_cast<uint32_t>(e + c)) : 0ull;
+      const bool t = ks > 0 && kk[c] != 0u && cc >= clo;
+      const uint64_t m = __ballot(t);
+      if (m) {
+        int base = 0;
+        if (lane == 0) base = atomicAdd(&sh.ints[8], __popcll(m));
+        base = __shfl(base, 0);
+        const int pos = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+        if (t && pos < kKmax) sh.top[pos] = cc;
+      }
+    }
+  }
+  if (tid < kKmax) sh.rank[tid] = 0;
+  __syncthreads();
+  const int nt = min(sh.ints[8], ks);
+  {
+    const int parts = nt <= 64 ? kTkW : kTkNT / max(nt, 1);
+    const int pw = nt <= 64 ? w : tid / max(nt, 1);
+    const int ci = nt <= 64 ? lane : tid % max(nt, 1);
+    if (nt > 0 && pw < parts && ci < nt) {
+      const int chunk = (nt + parts - 1) / parts;
+      const uint64_t x = sh.top[ci];
+      int r = 0;
+      const int j1 = min(nt, (pw + 1) * chunk);
+      for (int j = pw * chunk; j < j1; ++j) r += sh.top[j] > x;
+      if (r) atomicAdd(&sh.rank[ci], r);
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < nt; i += kTkNT)
+    __hip_atomic_store(&a.s_cand[slot * kKmax + sh.rank[i]], sh.top[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t np = 0;
+  if (a.info && pen) {
+    for (int i = tid; i < words; i += kTkNT) np += __popc(sh.bits[i]);
+    np = block_sum_u32<kTkNT>(np, sh.red32);
+  }
+  if (tid == 0) {
+    __hip_atomic_store(&a.s_cnt[slot], nt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&a.s_npen[slot], static_cast<int>(np), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // every store of this part has completed before its ticket is taken
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned t = __hip_atomic_fetch_add(&a.g_tick[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh.ints[9] = t == static_cast<unsigned>(a.P - 1);
+  }
+  __syncthreads();
+  if (!sh.ints[9]) return;
+  if (tid == 0) __hip_atomic_store(&a.g_tick[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  finish_smallk<kTkNT, true>(a, row, P, a.P, sh.mbuf, sh.top, sh.red64, sh.ints, sh.off);
+}
+
 // ---- split greedy rows: a small greedy batch, each row cut into parts over several CUs ----------
 //
 // With fewer rows than CUs, one workgroup per row leaves most of the chip idle. Here row r's 16-byte
@@ -2724,6 +2988,10 @@ __global__ __launch_bounds__(256) void k_exp_probe(const double* __restrict__ x,
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st) {
   const long long blocks = std::min<long long>((n + 255) / 256, 4096);
   hipLaunchKernelGGL(k_exp_probe, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, x, y, n);
+}
+
+void launch_topk_split(const KArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_topk_split, dim3(static_cast<unsigned>(a.B * a.P)), dim3(kTkNT), 0, st, a);
 }
 
 void launch_greedy_split(const KArgs& a, hipStream_t st) {
