@@ -117,7 +117,7 @@ struct Plan {
 };
 
 // VSMP_MODE=rows|slices|split pins the decomposition (testing and tuning); default: split parts
-// for a greedy batch of at most half as many rows as CUs, or a small-k batch of at most 8 long rows
+// for a greedy batch of at most half as many rows as CUs, or a small-k batch of at most 24 long rows
 // (topk_parts), else rows whenever the vocabulary fits the row kernel (V <= 2^19), slices beyond.
 // split applies to greedy and small-k batches with shared parameters only; other batches take the
 // default.
@@ -151,22 +151,23 @@ int split_parts(int B, int V, int cus, bool forced) {
 
 // Parts per row of a split small-k batch: the fewest parts of at most kSplitMaxPartGroups groups
 // (a part's cost is mostly fixed, and the last part merges one list per part), within what the last
-// part can merge (at most kMaxMergeSlices lists, P * k <= kMergeCap entries). 0: no split.
+// part can merge: a part's list holds up to kKmax entries (all its keys above its bound, when they
+// fit), so P * kKmax <= kMergeCap. 0: no split.
 int topk_parts(int B, int V, int cus, int k, bool forced) {
   const long long V4 = (static_cast<long long>(V) + 3) / 4;
   const long long pmin = (V4 + kSplitMaxPartGroups - 1) / kSplitMaxPartGroups;
-  const long long kk = std::max(1, std::min(k, kKmax));
-  const long long pmax = std::min<long long>({std::max(pmin, V4 / 512), kMaxMergeSlices, kMergeCap / kk});
+  const long long pmax = std::min<long long>({std::max(pmin, V4 / 512), kMaxMergeSlices, kMergeCap / kKmax});
   if (pmin > pmax) return 0;
   static const long long forced_p = [] {
     const char* e = std::getenv("VSMP_SPLIT_P");
     return e ? std::atoll(e) : 0LL;
   }();
   const long long P = forced_p > 0 ? std::min(std::max(forced_p, pmin), pmax) : pmin;
-  // Measured against row mode (top-k 40, V = 151936): faster at B = 1 and 8 (18.8 / 20.4 against
-  // 21.5 / 22.8 us), even at 16, slower from 32 on; slower at any B when the row is short (one
-  // workgroup streams it quickly: V = 49152, 17.8 against 14.0 us). Default: B <= 8, P >= 8.
-  if (!forced && (B > 8 || P < 8)) return 0;
+  // Measured against row mode (top-k 40, V = 151936): faster up to B = 24 (1: 17.9 against 21.5,
+  // 8: 18.6 / 22.8, 16: 20.7 / 22.6, 24: 20.5 / 23.1 us), even at 32 (22.8 / 23.0); slower at any B
+  // when the row is short (one workgroup streams it quickly: V = 49152, 17.8 against 14.0 us).
+  // Default: B <= 24, P >= 8.
+  if (!forced && (B > 24 || P < 8)) return 0;
   if (static_cast<long long>(B) * P > INT32_MAX) return 0;
   return static_cast<int>(std::max<long long>(P, 1));
 }

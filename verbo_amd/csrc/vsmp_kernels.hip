@@ -1067,10 +1067,13 @@ __device__ void finish_smallk(const KArgs& a, int row, const vsmp_params& P, int
     }
 #pragma unroll
     for (int j = 0; j < PF; ++j)
-      if (i0 + j * NT + tid < M && vals[j] >= lb) sm_buf[atomicAdd(&sm_int[7], 1)] = vals[j];
+      if (i0 + j * NT + tid < M && vals[j] >= lb) {
+        const int pos = atomicAdd(&sm_int[7], 1);
+        if (pos < kMergeCap) sm_buf[pos] = vals[j];  // M <= kMergeCap by the plan
+      }
   }
   __syncthreads();
-  const int C = sm_int[7];  // >= k
+  const int C = min(sm_int[7], kMergeCap);  // >= k
   if (C <= 2 * NT) {
     // rank by counting (composites are distinct)
     pad16(sm_buf, C, tid);
@@ -2719,11 +2722,43 @@ __global__ __launch_bounds__(kTkNT) void k_topk_split(KArgs a) {
     __syncthreads();
   }
 
-  // the exact ks-th largest composite: 2048-bin passes over the composites >= T << 32 in registers,
-  // each narrowing [lo, hi] to the bucket that holds it, until the bucket is taken whole
-  uint64_t clo = static_cast<uint64_t>(T) << 32, chi = mxc;
+  // the part's list: every composite >= clo, collected in LDS (at most kKmax kept)
+  auto collect = [&](uint64_t clo) {
+#pragma unroll
+    for (int u = 0; u < kTkU; ++u) {
+      const uint32_t kk[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      const int e = 4 * (g0 + u * kTkNT + tid);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint64_t cc = kk[c] ? comp(kk[c], static_cast<uint32_t>(e + c)) : 0ull;
+        const bool t = ks > 0 && kk[c] != 0u && cc >= clo;
+        const uint64_t m = __ballot(t);
+        if (m) {
+          int base = 0;
+          if (lane == 0) base = atomicAdd(&sh.ints[8], __popcll(m));
+          base = __shfl(base, 0);
+          const int pos = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+          if (t && pos < kKmax) sh.top[pos] = cc;
+        }
+      }
+    }
+  };
+  // Usually the keys above the bound fit the list: it is kept whole (the merge takes the row's top
+  // k from the union of the lists, each sorted). Otherwise the exact ks-th largest composite is found
+  // first: 2048-bin passes over the composites >= T << 32 in registers, each narrowing [clo, chi]
+  // to the bucket that holds it, until the bucket is taken whole; the list is then exactly ks long.
+  uint32_t nabove = 0;
+#pragma unroll
+  for (int u = 0; u < kTkU; ++u)
+    nabove += (v[u].x >= T && v[u].x != 0u) + (v[u].y >= T && v[u].y != 0u) + (v[u].z >= T && v[u].z != 0u) +
+              (v[u].w >= T && v[u].w != 0u);
+  nabove = block_sum_u32<kTkNT>(nabove, sh.red32);
+  uint64_t clo = static_cast<uint64_t>(T) << 32;
+  if (ks > 0 && nabove > static_cast<uint32_t>(kKmax)) {
+  uint64_t chi = mxc;
   int need = ks;
-  for (int pass = 0; ks > 0 && clo != chi && pass < 9; ++pass) {
+  for (int pass = 0; clo != chi && pass < 9; ++pass) {
     const uint64_t R = chi - clo;
     const int sft = R < static_cast<uint64_t>(kRowBins) ? 0 : 53 - __clzll(static_cast<long long>(R));
     uint32_t* bins = sh.bins[pass & 1];
@@ -2753,30 +2788,11 @@ __global__ __launch_bounds__(kTkNT) void k_topk_split(KArgs a) {
     clo = nlo;
     if (inb == need) chi = clo;  // the whole bucket is taken: the top ks are the composites >= clo
   }
-
-  // collect the composites >= clo (exactly ks of them), rank them and store them sorted
-#pragma unroll
-  for (int u = 0; u < kTkU; ++u) {
-    const uint32_t kk[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-    const int e = 4 * (g0 + u * kTkNT + tid);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint64_t cc = kk[c] ? comp(kk[c], static_cast<uint32_t>(e + c)) : 0ull;
-      const bool t = ks > 0 && kk[c] != 0u && cc >= clo;
-      const uint64_t m = __ballot(t);
-      if (m) {
-        int base = 0;
-        if (lane == 0) base = atomicAdd(&sh.ints[8], __popcll(m));
-        base = __shfl(base, 0);
-        const int pos = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
-        if (t && pos < kKmax) sh.top[pos] = cc;
-      }
-    }
   }
+  collect(clo);
   if (tid < kKmax) sh.rank[tid] = 0;
   __syncthreads();
-  const int nt = min(sh.ints[8], ks);
+  const int nt = min(sh.ints[8], kKmax);
   {
     const int parts = nt <= 64 ? kTkW : kTkNT / max(nt, 1);
     const int pw = nt <= 64 ? w : tid / max(nt, 1);
