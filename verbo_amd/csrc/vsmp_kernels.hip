@@ -2513,6 +2513,9 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
       hi = (hi0 - lo < wdt) ? hi0 : lo + wdt;
     }
     if (b < 0 || inb == need) hi = lo;  // done (b < 0 is unreachable: ks composites lie at or above lo0)
+    // A bucket that holds more than the ks-th is taken whole when it and the buckets above it fit
+    // the candidate list: the ranks below then keep the top ks, so no refinement pass is needed.
+    if (sh.ints[1] + inb <= kKmax) hi = lo;
   }
   for (int pass = 1; lo != hi && pass < 9; ++pass) {
     const uint64_t R = hi - lo;
@@ -2537,7 +2540,7 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     if (inb == need) hi = lo;  // the whole bucket is taken: the top ks are the composites >= lo
   }
 
-  // -- collect the composites >= lo (exactly ks of them)
+  // -- collect the composites >= lo (ks of them, or up to kKmax when a bucket was taken whole)
   for (int i0 = 0; i0 < cnt; i0 += 64) {
     const int i = i0 + lane;
     const uint64_t c = i < cnt ? buf[i] : 0ull;
@@ -2553,35 +2556,38 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     }
   }
   __syncthreads();
-  const int nt = min(sh.ints[8], ks);
+  const int nc = min(sh.ints[8], kKmax);  // collected
+  const int nt = min(nc, ks);             // kept: the nt largest of them
 
   // -- ranks (composites are distinct): every thread counts the entries above one candidate in a
-  // share of the list; then wave 0 places them and runs the reference epilogue
+  // share of the list; then wave 0 places the top nt and runs the reference epilogue
   {
     const int i = tid & 63;
-    const int parts = nt <= 64 ? kRowW : kRowNT / nt;
-    const int part = nt <= 64 ? w : tid / nt;
-    const int ci = nt <= 64 ? i : tid % nt;
-    if (part < parts && ci < nt) {
-      const int chunk = (nt + parts - 1) / parts;
+    const int parts = nc <= 64 ? kRowW : kRowNT / nc;
+    const int part = nc <= 64 ? w : tid / nc;
+    const int ci = nc <= 64 ? i : tid % nc;
+    if (part < parts && ci < nc) {
+      const int chunk = (nc + parts - 1) / parts;
       const uint64_t x = sh.top[ci];
       int r = 0;
-      const int j1 = min(nt, (part + 1) * chunk);
+      const int j1 = min(nc, (part + 1) * chunk);
       for (int j = part * chunk; j < j1; ++j) r += sh.top[j] > x;
       if (r) atomicAdd(&sh.rank[ci], r);
     }
     // wave 0 also takes the numerators (src/sampler.cpp:79-83), in collection order
     if (w == 0) {
       const float mx = comp_val(maxc);
-      for (int j = lane; j < nt; j += 64) sh.top_pr[j] = numer(comp_val(sh.top[j]), mx, P.temp);
+      for (int j = lane; j < nc; j += 64) sh.top_pr[j] = numer(comp_val(sh.top[j]), mx, P.temp);
     }
   }
   __syncthreads();
   if (w == 0) {
-    for (int i = lane; i < nt; i += 64) {
+    for (int i = lane; i < nc; i += 64) {
       const int r = sh.rank[i];
-      sh.sorted[r] = sh.top[i];
-      sh.spr[r] = sh.top_pr[i];
+      if (r < nt) {
+        sh.sorted[r] = sh.top[i];
+        sh.spr[r] = sh.top_pr[i];
+      }
     }
     wave_lds_sync();
     if (nt <= 64)
