@@ -2031,6 +2031,27 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return static_cast<uint32_t>(__builtin_amdgcn_readlane(x, 63));
 }
 
+// Maximum of a 64-bit value over the 64 lanes of a wave, by DPP row shifts and broadcasts (lanes
+// without a source keep 0, which no maximum here is below); uniform result.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#define VSMP_DPP_MAX64(ctrl, rm)                                                                              \
+  {                                                                                                     \
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(v), ctrl, rm, 0xf, false);            \
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), ctrl, rm, 0xf, false);      \
+    v = max64(v, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo)); \
+  }
+  VSMP_DPP_MAX64(0x111, 0xf);
+  VSMP_DPP_MAX64(0x112, 0xf);
+  VSMP_DPP_MAX64(0x114, 0xf);
+  VSMP_DPP_MAX64(0x118, 0xf);
+  VSMP_DPP_MAX64(0x142, 0xa);
+  VSMP_DPP_MAX64(0x143, 0xc);
+#undef VSMP_DPP_MAX64
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), 63));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 // One wave searches 2048 bins from the top (bucket 2047 first) for the first bucket whose running
 // count reaches `need` (such a bucket is never empty). Lane l first sums buckets 2047-32l down to
 // 2016-32l; a scan over lanes finds the 32 buckets holding the crossing, and a second scan over
@@ -2458,7 +2479,7 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     wmx = max64(wmx, c);
     if (path != kPathGreedy && c >= lo0) atomicAdd(&sh.bins[0][c > hi0 ? 2047 : (c - lo0) >> s0], 1u);
   }
-  for (int o = 32; o > 0; o >>= 1) wmx = max64(wmx, __shfl_xor(wmx, o));
+  wmx = wave_max_u64(wmx);
   uint32_t np = 0;
   if (a.info && pen) {
     for (int i = tid; i < words; i += kRowNT) np += __popc(bits[i]);
