@@ -2569,7 +2569,7 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     const uint64_t m = __ballot(t);
     int base = 0;
     if (lane == 0 && m) base = atomicAdd(&sh.ints[8], __popcll(m));
-    base = __shfl(base, 0);
+    base = __builtin_amdgcn_readfirstlane(base);  // lane 0: every lane is active here
     if (t) {
       const int p = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
                                                                       __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
@@ -2763,7 +2763,7 @@ __global__ __launch_bounds__(kTkNT) void k_topk_split(KArgs a) {
         if (m) {
           int base = 0;
           if (lane == 0) base = atomicAdd(&sh.ints[8], __popcll(m));
-          base = __shfl(base, 0);
+          base = __builtin_amdgcn_readfirstlane(base);  // lane 0: every lane is active here
           const int pos = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
                                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
           if (t && pos < kKmax) sh.top[pos] = cc;
