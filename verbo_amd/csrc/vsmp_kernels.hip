@@ -1156,6 +1156,8 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
 
 constexpr int kGenNW = kGenThreads / 64;
 constexpr int kRefBuckets = 2048;
+static_assert(kGenBuckets % kGenThreads == 0 && kRefBuckets % kGenThreads == 0, "whole buckets per thread");
+static_assert(kGenCap <= 2 * kGenThreads, "lists of up to kGenCap entries are scanned two per thread");
 
 struct GenRow {
   const float* rp;
@@ -1465,37 +1467,66 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, PV&
       if (MASS) atomicAdd(&sh.rmass[d], numer_g(g, v));
     });
     __syncthreads();
-    // scan buckets from the top (largest composites first): position p <-> bucket 2047 - p
-    const int p0 = 2 * tid;
-    const int d0 = kRefBuckets - 1 - p0, d1 = d0 - 1;
-    const double m0 = MASS ? sh.rmass[d0] : static_cast<double>(sh.rcnt[d0]);
-    const double m1 = MASS ? sh.rmass[d1] : static_cast<double>(sh.rcnt[d1]);
-    const uint32_t c0 = sh.rcnt[d0], c1 = sh.rcnt[d1];
+    // scan buckets from the top (largest composites first): position p <-> bucket kRefBuckets-1-p,
+    // RP consecutive positions per thread
+    constexpr int RP = kRefBuckets / kGenThreads;
+    const int p0 = RP * tid;
+    double mv[RP];
+    uint32_t cv[RP];
+    double ms = 0.0;
+    uint32_t cs = 0;
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+      const int d = kRefBuckets - 1 - (p0 + r);
+      cv[r] = sh.rcnt[d];
+      mv[r] = MASS ? sh.rmass[d] : static_cast<double>(cv[r]);
+      ms += mv[r];
+      cs += cv[r];
+    }
     double em;
     uint32_t ec;
-    block_excl_scan<kGenThreads>(m0 + m1, c0 + c1, em, ec, sh.wm, sh.wc);
+    block_excl_scan<kGenThreads>(ms, cs, em, ec, sh.wm, sh.wc);
     if (tid == 0) sh.ints[0] = kRefBuckets;
     __syncthreads();
     // first non-empty position whose inclusive weight reaches the target
-    const double i0 = above + em + m0, i1 = i0 + m1;
-    const bool k0 = c0 && i0 >= target, k1 = c1 && i1 >= target;
-    wave_claim_min(&sh.ints[0], k0 || k1, k0 ? p0 : p0 + 1);
+    int first = -1;
+    {
+      double run = above + em;
+#pragma unroll
+      for (int r = 0; r < RP; ++r) {
+        run += mv[r];
+        if (first < 0 && cv[r] && run >= target) first = p0 + r;
+      }
+    }
+    wave_claim_min(&sh.ints[0], first >= 0, first);
     __syncthreads();
     int pos = sh.ints[0];
     if (pos == kRefBuckets) {
       // target not reached (rounding): continue in the last non-empty bucket
       if (tid == 0) sh.ints[1] = -1;
       __syncthreads();
-      if (c0) atomicMax(&sh.ints[1], p0);
-      if (c1) atomicMax(&sh.ints[1], p0 + 1);
+      int last = -1;
+#pragma unroll
+      for (int r = 0; r < RP; ++r)
+        if (cv[r]) last = p0 + r;
+      if (last >= 0) atomicMax(&sh.ints[1], last);
       __syncthreads();
       pos = sh.ints[1];
     }
     // owner of `pos` publishes the weight / count before it
-    if (pos == p0 || pos == p0 + 1) {
-      sh.dbls[0] = above + em + (pos == p0 ? 0.0 : m0);
-      sh.ints[2] = rank_above + static_cast<int>(ec) + (pos == p0 ? 0 : static_cast<int>(c0));
-      sh.ints[3] = static_cast<int>(pos == p0 ? c0 : c1);
+    if (pos >= p0 && pos < p0 + RP) {
+      double before = above + em;
+      uint32_t cb = ec;
+#pragma unroll
+      for (int r = 0; r < RP; ++r) {
+        if (p0 + r == pos) {
+          sh.dbls[0] = before;
+          sh.ints[2] = rank_above + static_cast<int>(cb);
+          sh.ints[3] = static_cast<int>(cv[r]);
+        }
+        before += mv[r];
+        cb += cv[r];
+      }
     }
     __syncthreads();
     above = sh.dbls[0];
@@ -1710,12 +1741,14 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   };
   // level-0 inclusive prefixes (4 buckets per thread, bucket 0 = closest to the maximum)
   {
-    const int b0 = 4 * tid;
-    double m[4];
-    uint32_t c[4];
+    constexpr int BP = kGenBuckets / kGenThreads;  // consecutive buckets per thread
+    const int b0 = BP * tid;
+    double m[BP];
+    uint32_t c[BP];
     double ms = 0.0;
     uint32_t cs = 0;
-    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
       m[i] = sh.mass0[b0 + i];
       c[i] = sh.cnt0[b0 + i];
       ms += m[i];
@@ -1724,7 +1757,8 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     double em;
     uint32_t ec;
     block_excl_scan<kGenThreads>(ms, cs, em, ec, sh.wm, sh.wc);
-    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
       em += m[i];
       ec += c[i];
       sh.mass0[b0 + i] = em;
