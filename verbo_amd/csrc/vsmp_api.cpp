@@ -114,6 +114,7 @@ struct Plan {
   int P;
   int ept, S, L, grid, xcd, smallk_ok;
   bool any_general, any_smallk, any_finish;
+  bool no_rows_kernel;  // row mode with every row general: k_general alone takes the batch
 };
 
 // VSMP_MODE=rows|slices|split pins the decomposition (testing and tuning); default: split parts
@@ -210,6 +211,12 @@ Plan plan(int B, int V, const vsmp_params* hostp, int cus) {
     } else {
       pl.any_general = true;
     }
+    // A batch of general rows only is taken whole by k_general (its own maximum / minimum pass and
+    // bitmap), so that each row's passes follow one another while it is still in the Infinity
+    // Cache: 243 against 263 us at 512 x 151936 (top-k 0). Mixed batches keep k_rows's pass over
+    // their general rows, which spreads it over the whole launch (fused: 230 against 223 us at
+    // 1024 x 128256 with per-row parameters).
+    pl.no_rows_kernel = hostp && pl.any_general;
     pl.any_smallk = false;
     pl.any_finish = false;
     return pl;
@@ -281,7 +288,8 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
       !grow(ctx->s_max, ctx->n_max, slots, false, "scratch") || !grow(ctx->s_min, ctx->n_min, slots, false, "scratch"))
     return -1;
   if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch")) return -1;
-  if (pl.any_general && hist && !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch"))
+  if (pl.any_general && hist && !pl.no_rows_kernel &&
+      !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch"))
     return -1;
 
   KArgs a{};
@@ -317,6 +325,7 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   a.s_min = ctx->s_min;
   a.s_bits = ctx->s_bits;
   a.words = words;
+  a.gen_fused = pl.no_rows_kernel ? 1 : 0;
   if (pl.split) {
     if (!grow(ctx->g_slot, ctx->n_slot, static_cast<size_t>(B), true, "scratch") ||
         !grow(ctx->g_tick, ctx->n_tick, static_cast<size_t>(B), true, "scratch") ||
@@ -333,8 +342,10 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
     return hip_ok(hipGetLastError(), "split launch") ? 0 : -1;
   }
   if (pl.rows) {
-    launch_rows(a, st);
-    if (!hip_ok(hipGetLastError(), "row launch")) return -1;
+    if (!pl.no_rows_kernel) {
+      launch_rows(a, st);
+      if (!hip_ok(hipGetLastError(), "row launch")) return -1;
+    }
   } else {
     launch_stage1(a, pl.ept, pl.grid, st);
     if (!hip_ok(hipGetLastError(), "stage-1 launch")) return -1;

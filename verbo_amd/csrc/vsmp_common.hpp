@@ -55,6 +55,8 @@ struct KArgs {
   unsigned int* s_min;         // [B*S] slice minimum (order key)
   unsigned int* s_bits;        // [B][words] penalty bitmaps of general-path rows
   int words;                   // bitmap words per row
+  int gen_fused;               // 1 (row mode, every row general): k_general takes its rows' maximum,
+                               // minimum and penalty bitmap itself, and k_rows leaves general rows alone
   // split greedy rows: P parts per row; per-row slot (largest composite), ticket and penalised-id
   // count, all zero between calls (the last part of a row clears them)
   int P;

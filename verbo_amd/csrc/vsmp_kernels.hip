@@ -1592,15 +1592,6 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   const int S = a.S;
   exp_tab_fill();  // ordered before its first use by the barriers of the reductions below
 
-  // row maximum / minimum from the slices
-  uint64_t mxc = 0ull, mnk = ~0ull;
-  for (int i = tid; i < S; i += kGenThreads) {
-    mxc = max64(mxc, a.s_max[row * S + i]);
-    mnk = min64(mnk, a.s_min[row * S + i]);
-  }
-  mxc = block_max64<kGenThreads>(mxc, sh.r64);
-  mnk = block_min64<kGenThreads>(mnk, sh.r64);
-
   int h0 = 0, h1 = 0;
   if (a.hist_off) {
     h0 = a.hist_off[row];
@@ -1613,12 +1604,47 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   g.R.rep = P.repeat;
   g.R.bits = a.s_bits + static_cast<size_t>(row) * a.words;
   g.R.lds_bits = false;
-  if (g.R.pen && static_cast<size_t>(a.words) * sizeof(uint32_t) <= kGenBitsLds) {  // the launch's rule
-    uint32_t* lb = gen_lds_bits();
-    for (int i = tid; i < a.words; i += kGenThreads) lb[i] = g.R.bits[i];
-    __syncthreads();
-    g.R.lds_bits = true;
+  uint64_t mxc = 0ull, mnk = ~0ull;
+  if (a.gen_fused) {
+    // Row mode: the penalty bitmap (src/sampler.cpp:53-65) straight into LDS (it fits: V <= 2^19),
+    // then one pass for the row maximum and minimum. The row's later passes follow soon enough to
+    // find much of it still in the Infinity Cache.
+    if (g.R.pen) {
+      uint32_t* lb = gen_lds_bits();
+      for (int i = tid; i < a.words; i += kGenThreads) lb[i] = 0u;
+      __syncthreads();
+      const int H = h1 - h0;
+      const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
+      for (int i = hfrom + tid; i < h1; i += kGenThreads) {
+        const int id = a.hist[i];
+        if (id >= 0 && id < V) atomicOr(&lb[id >> 5], 1u << (id & 31));
+      }
+      __syncthreads();
+      g.R.bits = lb;
+      g.R.lds_bits = true;
+    }
+    uint32_t mn = 0xFFFFFFFFu;
+    gen_pass(g.R, [&](int e, float v) {
+      const uint32_t kv = ord_key(v);
+      mxc = max64(mxc, comp(kv, static_cast<uint32_t>(e)));
+      mn = min(mn, kv);
+    });
+    mnk = mn;
+  } else {
+    // row maximum / minimum from the slices (or k_rows's pass), the bitmap from scratch
+    for (int i = tid; i < S; i += kGenThreads) {
+      mxc = max64(mxc, a.s_max[row * S + i]);
+      mnk = min64(mnk, a.s_min[row * S + i]);
+    }
+    if (g.R.pen && static_cast<size_t>(a.words) * sizeof(uint32_t) <= kGenBitsLds) {  // the launch's rule
+      uint32_t* lb = gen_lds_bits();
+      for (int i = tid; i < a.words; i += kGenThreads) lb[i] = g.R.bits[i];
+      __syncthreads();
+      g.R.lds_bits = true;
+    }
   }
+  mxc = block_max64<kGenThreads>(mxc, sh.r64);
+  mnk = block_min64<kGenThreads>(mnk, sh.r64);
   g.mx = comp_val(mxc);
   g.temp = P.temp;
   g.inv_temp = 1.0 / static_cast<double>(P.temp);
@@ -2368,6 +2394,7 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   if (tid == 0 && path == kPathSmallK) u0 = draw_u(a, row, P);
 
   if (path == kPathGeneral) {
+    if (a.gen_fused) return;  // k_general takes the whole row
     if (pen) {
       for (int i = tid; i < words; i += kRowNT) bits[i] = 0u;
       __syncthreads();
