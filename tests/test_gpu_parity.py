@@ -383,7 +383,9 @@ def test_graph_capture_and_replay(ctx):
     """vsmp_pick_batch captured into a HIP graph (after one eager call has sized the scratch) and
     replayed with new logits and draws copied into the captured buffers between replays: every
     replay equals the eager call on the same inputs, for a greedy batch (split mode), a top-k batch
-    (row mode) and a general batch (row mode + k_general), all three in one graph."""
+    (row mode), a general batch (k_general alone) and a batch with per-row parameters mixing top-k
+    and general rows (k_rows, and k_general on a stream forked from and joined back to the
+    capturing one), all four in one graph."""
     import torch
 
     rng = np.random.default_rng(51)
@@ -392,6 +394,10 @@ def test_graph_capture_and_replay(ctx):
              V.params_array(n=1, temp=0.8, top_k=40, top_p=0.9, min_p=0.02, repeat=1.1, repeat_last=0, seed=1),
              V.params_array(n=1, temp=1.0, top_k=0, top_p=0.95, repeat=1.1, repeat_last=0, seed=1)]
     prm = [V.Params(*[p[0][f].item() for f in V.SAMPLING_DTYPE.names]) for p in cases]
+    per_row = V.params_array(n=B, temp=0.9, top_k=40, top_p=0.9, repeat=1.1, repeat_last=0, seed=1)
+    per_row["top_k"][::2] = 0
+    cases.append(per_row)
+    prm.append(V.to_device_params(per_row))
     h, off = csr([list(rng.integers(0, Vv, 100)) for _ in range(B)])
     dh, doff = torch.from_numpy(h).cuda(), torch.from_numpy(off).cuda()
     lg = torch.zeros((B, Vv), dtype=torch.float32, device="cuda")

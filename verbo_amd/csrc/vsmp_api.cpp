@@ -69,6 +69,10 @@ struct vsmp_ctx {
   int device = 0;
   int cus = 256;                 // compute units of the device
   hipStream_t stream = nullptr;  // used by the host-pointer path
+  // row mode with per-row parameters: k_general runs on `side`, forked from and joined back to the
+  // caller's stream by the two events, next to k_rows
+  hipStream_t side = nullptr;
+  hipEvent_t fork_ev = nullptr, join_ev = nullptr;
   // batched-path scratch
   unsigned long long* s_cand = nullptr;
   size_t n_cand = 0;
@@ -115,6 +119,7 @@ struct Plan {
   int ept, S, L, grid, xcd, smallk_ok;
   bool any_general, any_smallk, any_finish;
   bool no_rows_kernel;  // row mode with every row general: k_general alone takes the batch
+  bool side_general;    // row mode with per-row parameters: k_general next to k_rows, on a side stream
 };
 
 // VSMP_MODE=rows|slices|split pins the decomposition (testing and tuning); default: split parts
@@ -217,6 +222,10 @@ Plan plan(int B, int V, const vsmp_params* hostp, int cus) {
     // their general rows, which spreads it over the whole launch (fused: 230 against 223 us at
     // 1024 x 128256 with per-row parameters).
     pl.no_rows_kernel = hostp && pl.any_general;
+    // With per-row parameters k_general takes its rows whole as well and runs next to k_rows (which
+    // leaves those rows alone), on a stream forked from the caller's: the few long general rows
+    // then overlap the row kernel instead of following it.
+    pl.side_general = !hostp;
     pl.any_smallk = false;
     pl.any_finish = false;
     return pl;
@@ -288,7 +297,7 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
       !grow(ctx->s_max, ctx->n_max, slots, false, "scratch") || !grow(ctx->s_min, ctx->n_min, slots, false, "scratch"))
     return -1;
   if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch")) return -1;
-  if (pl.any_general && hist && !pl.no_rows_kernel &&
+  if (pl.any_general && hist && !pl.rows &&
       !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch"))
     return -1;
 
@@ -325,7 +334,7 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   a.s_min = ctx->s_min;
   a.s_bits = ctx->s_bits;
   a.words = words;
-  a.gen_fused = pl.no_rows_kernel ? 1 : 0;
+  a.gen_fused = pl.rows ? 1 : 0;
   if (pl.split) {
     if (!grow(ctx->g_slot, ctx->n_slot, static_cast<size_t>(B), true, "scratch") ||
         !grow(ctx->g_tick, ctx->n_tick, static_cast<size_t>(B), true, "scratch") ||
@@ -340,6 +349,17 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
     else
       launch_greedy_split(a, st);
     return hip_ok(hipGetLastError(), "split launch") ? 0 : -1;
+  }
+  if (pl.rows && pl.side_general) {
+    if (!hip_ok(hipEventRecord(ctx->fork_ev, st), "hipEventRecord") ||
+        !hip_ok(hipStreamWaitEvent(ctx->side, ctx->fork_ev, 0), "hipStreamWaitEvent"))
+      return -1;
+    launch_general(a, ctx->side);
+    if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
+    if (!hip_ok(hipEventRecord(ctx->join_ev, ctx->side), "hipEventRecord")) return -1;
+    launch_rows(a, st);
+    if (!hip_ok(hipGetLastError(), "row launch")) return -1;
+    return hip_ok(hipStreamWaitEvent(st, ctx->join_ev, 0), "hipStreamWaitEvent") ? 0 : -1;
   }
   if (pl.rows) {
     if (!pl.no_rows_kernel) {
@@ -379,8 +399,11 @@ vsmp_ctx* vsmp_ctx_new(int device) {
   c->device = dev;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) c->cus = cus;
-  if (!vsmp::hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate")) {
-    delete c;
+  if (!vsmp::hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate") ||
+      !vsmp::hip_ok(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking), "hipStreamCreate") ||
+      !vsmp::hip_ok(hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming), "hipEventCreate") ||
+      !vsmp::hip_ok(hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming), "hipEventCreate")) {
+    vsmp_ctx_free(c);
     return nullptr;
   }
   return c;
@@ -395,6 +418,9 @@ void vsmp_ctx_free(vsmp_ctx* c) {
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->stream) (void)hipStreamDestroy(c->stream);
+  if (c->side) (void)hipStreamDestroy(c->side);
+  if (c->fork_ev) (void)hipEventDestroy(c->fork_ev);
+  if (c->join_ev) (void)hipEventDestroy(c->join_ev);
   delete c;
 }
 
