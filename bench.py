@@ -110,8 +110,8 @@ def main():
                          "that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: the sampler has no multi-GPU path in this build (asked for "
-              f"--gpus {args.gpus}). Rows are independent; sharding is described in DESIGN.md.", file=sys.stderr)
+        print(f"bench.py measures one GPU: the sampler has no multi-GPU path (asked for --gpus {args.gpus}). "
+              f"Rows are independent, so each GPU would take its own share of the batch's rows.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -1,7 +1,7 @@
 """Shared test helpers: run the HIP sampler through the C ABI and the oracle on the same inputs,
 then compare with the reference's tolerance rules.
 
-Comparison rules (the north-star parity bar):
+Comparison rules (the parity bar):
 - greedy ids, penalised sets, top-k/min-p/top-p candidate sets: bit-exact, except where the
   oracle's own decision margin is below rounding distance (|acc - top_p| < 1e-11,
   |pr - thr| / thr < 1e-13), which are counted;
