@@ -355,11 +355,15 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
         !hip_ok(hipStreamWaitEvent(ctx->side, ctx->fork_ev, 0), "hipStreamWaitEvent"))
       return -1;
     launch_general(a, ctx->side);
-    if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
+    bool ok = hip_ok(hipGetLastError(), "general-path launch");
     if (!hip_ok(hipEventRecord(ctx->join_ev, ctx->side), "hipEventRecord")) return -1;
-    launch_rows(a, st);
-    if (!hip_ok(hipGetLastError(), "row launch")) return -1;
-    return hip_ok(hipStreamWaitEvent(st, ctx->join_ev, 0), "hipStreamWaitEvent") ? 0 : -1;
+    if (ok) {
+      launch_rows(a, st);
+      ok = hip_ok(hipGetLastError(), "row launch");
+    }
+    // joined in every case, so that nothing of this call runs unordered with the caller's stream
+    if (!hip_ok(hipStreamWaitEvent(st, ctx->join_ev, 0), "hipStreamWaitEvent")) return -1;
+    return ok ? 0 : -1;
   }
   if (pl.rows) {
     if (!pl.no_rows_kernel) {
