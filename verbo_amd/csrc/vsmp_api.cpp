@@ -80,6 +80,13 @@ struct vsmp_ctx {
   size_t n_cnt = 0;
   int* s_npen = nullptr;
   size_t n_npen = 0;
+  // exact redo of general rows marked near a top-p tie (k_general_exact)
+  int* x_flag = nullptr;
+  size_t n_xflag = 0;
+  double* x_u = nullptr;
+  size_t n_xu = 0;
+  unsigned long long* x_buf = nullptr;
+  size_t n_xbuf = 0;
   unsigned long long* s_max = nullptr;
   size_t n_max = 0;
   unsigned int* s_min = nullptr;
@@ -297,6 +304,14 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
       !grow(ctx->s_max, ctx->n_max, slots, false, "scratch") || !grow(ctx->s_min, ctx->n_min, slots, false, "scratch"))
     return -1;
   if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch")) return -1;
+  // general rows marked near a top-p tie are redone exactly (rows up to kExactMaxVocab)
+  const bool exact = pl.any_general && V <= kExactMaxVocab;
+  int x_n = 1;
+  while (x_n < V) x_n <<= 1;
+  if (exact && (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch") ||
+                !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch") ||
+                !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(kExactSlots) * 2 * x_n, false, "scratch")))
+    return -1;
   if (pl.any_general && hist && !pl.rows &&
       !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch"))
     return -1;
@@ -335,6 +350,10 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   a.s_bits = ctx->s_bits;
   a.words = words;
   a.gen_fused = pl.rows ? 1 : 0;
+  a.x_flag = exact ? ctx->x_flag : nullptr;
+  a.x_u = ctx->x_u;
+  a.x_buf = ctx->x_buf;
+  a.x_n = x_n;
   if (pl.split) {
     if (!grow(ctx->g_slot, ctx->n_slot, static_cast<size_t>(B), true, "scratch") ||
         !grow(ctx->g_tick, ctx->n_tick, static_cast<size_t>(B), true, "scratch") ||
@@ -356,6 +375,10 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
       return -1;
     launch_general(a, ctx->side);
     bool ok = hip_ok(hipGetLastError(), "general-path launch");
+    if (ok && exact) {
+      launch_general_exact(a, ctx->side);
+      ok = hip_ok(hipGetLastError(), "exact general-path launch");
+    }
     if (!hip_ok(hipEventRecord(ctx->join_ev, ctx->side), "hipEventRecord")) return -1;
     if (ok) {
       launch_rows(a, st);
@@ -381,6 +404,10 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   if (pl.any_general) {
     launch_general(a, st);
     if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
+    if (exact) {
+      launch_general_exact(a, st);
+      if (!hip_ok(hipGetLastError(), "exact general-path launch")) return -1;
+    }
   }
   return 0;
 }
@@ -417,7 +444,7 @@ void vsmp_ctx_free(vsmp_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
-  void* bufs[] = {c->s_cand, c->s_cnt, c->s_npen, c->s_max, c->s_min, c->s_bits, c->g_slot, c->g_tick,
+  void* bufs[] = {c->x_flag, c->x_u, c->x_buf, c->s_cand, c->s_cnt, c->s_npen, c->s_max, c->s_min, c->s_bits, c->g_slot, c->g_tick,
                   c->g_npen, c->d_logits, c->d_hist, c->d_hoff, c->d_u, c->d_out, c->d_info};
   for (void* p : bufs)
     if (p) (void)hipFree(p);

@@ -55,6 +55,13 @@ struct KArgs {
   unsigned int* s_min;         // [B*S] slice minimum (order key)
   unsigned int* s_bits;        // [B][words] penalty bitmaps of general-path rows
   int words;                   // bitmap words per row
+  // general rows whose top-p cut lay within rounding distance of top_p: k_general marks them
+  // (x_flag) with the draw it used (x_u), and k_general_exact redoes them in the reference's order
+  // and sequential sums, sorting each in one of kExactSlots scratch slots of 2 * x_n entries
+  int* x_flag;
+  double* x_u;
+  unsigned long long* x_buf;
+  int x_n;                     // a power of two >= V
   int gen_fused;               // 1 (row mode, every row general): k_general takes its rows' maximum,
                                // minimum and penalty bitmap itself, and k_rows leaves general rows alone
   // split greedy rows: P parts per row; per-row slot (largest composite), ticket and penalised-id
@@ -71,6 +78,9 @@ void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st);
 void launch_finish(const KArgs& a, hipStream_t st);
 void launch_rows(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
+void launch_general_exact(const KArgs& a, hipStream_t st);
+constexpr int kExactSlots = 8;            // workgroups (and scratch slots) of k_general_exact
+constexpr int kExactMaxVocab = 1 << 20;   // k_general_exact's reach (larger rows keep the flag)
 void launch_read_probe(const void* p, long long n16, unsigned* sink, int grid, hipStream_t st);
 void launch_greedy_split(const KArgs& a, hipStream_t st);
 void launch_topk_split(const KArgs& a, hipStream_t st);

@@ -2010,6 +2010,10 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   margin = tot > 0.0 ? margin / tot : 0.0;
   if (margin < kNearDraw) flags |= VSMP_FLAG_DRAW_NEAR;
   if (tid == 0) {
+    if (a.x_flag) {
+      a.x_flag[row] = (flags & VSMP_FLAG_TOPP_NEAR) ? 1 : 0;
+      a.x_u[row] = u;
+    }
     a.out[row] = id;
     if (a.info) {
       vsmp_row_info inf;
@@ -2029,6 +2033,146 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       inf.draw_margin = margin;
       a.info[row] = inf;
     }
+  }
+}
+
+// ---- exact redo of general rows whose top-p cut lies at rounding distance of top_p ------------
+//
+// k_general takes the top-p cut on fp64 sums in bucket order, which decide exactly only away from
+// the boundary; a row it marks (x_flag: the cut lay within kNearTopP of top_p, as on rows of
+// exactly tied logits) is redone here the reference's way (src/sampler.cpp:71-108): the row's
+// composites sorted in the reference's order (value descending, index ascending) by a bitonic
+// sort in a scratch slot, the numerators, then the sums by one thread in sorted order. Workgroup w
+// owns slot w and takes rows w, w + kExactSlots, ...: each thread reads one row's mark, and the
+// marked rows are gathered in LDS and redone one after the other. Slow by design (milliseconds
+// per marked row) and rare; a call without marked rows costs one read per row.
+__global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
+  __shared__ int list[kGenThreads];
+  __shared__ int nlist;
+  const int tid = threadIdx.x;
+  const int V = a.V, n2 = a.x_n;
+  uint64_t* xs = reinterpret_cast<uint64_t*>(a.x_buf) + static_cast<size_t>(blockIdx.x) * 2 * static_cast<size_t>(n2);
+  double* pr = reinterpret_cast<double*>(xs + n2);
+  for (int c0 = blockIdx.x; c0 < a.B; c0 += gridDim.x * kGenThreads) {
+    if (tid == 0) nlist = 0;
+    __syncthreads();
+    {
+      const int r = c0 + static_cast<int>(gridDim.x) * tid;
+      if (r < a.B && a.x_flag[r] != 0 && path_of(row_params(a, r), V, a.smallk_ok) == kPathGeneral)
+        list[atomicAdd(&nlist, 1)] = r;
+    }
+    __syncthreads();
+    const int nmarked = nlist;
+    for (int q = 0; q < nmarked; ++q) {
+      const int row = list[q];
+      const vsmp_params P = row_params(a, row);
+      int h0 = 0, h1 = 0;
+      if (a.hist_off) {
+        h0 = a.hist_off[row];
+        h1 = a.hist_off[row + 1];
+      }
+      GenRow R;
+      R.rp = a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld);
+      R.V = V;
+      R.pen = (P.repeat != 1.0f) && (h1 - h0) > 0;
+      R.rep = P.repeat;
+      R.bits = a.s_bits + static_cast<size_t>(row) * a.words;  // slice mode: stage 1 wrote it
+      R.lds_bits = false;
+      if (R.pen && a.gen_fused) {  // row mode: the bitmap in LDS, as k_general builds it
+        uint32_t* lb = gen_lds_bits();
+        for (int i = tid; i < a.words; i += kGenThreads) lb[i] = 0u;
+        __syncthreads();
+        const int H = h1 - h0;
+        const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
+        for (int i = hfrom + tid; i < h1; i += kGenThreads) {
+          const int id = a.hist[i];
+          if (id >= 0 && id < V) atomicOr(&lb[id >> 5], 1u << (id & 31));
+        }
+        __syncthreads();
+        R.bits = lb;
+        R.lds_bits = true;
+      }
+      // composites of the penalised row, zero-padded to n2, sorted descending (they are distinct)
+      gen_pass(R, [&](int e, float v) { xs[e] = comp(ord_key(v), static_cast<uint32_t>(e)); });
+      for (int i = V + tid; i < n2; i += kGenThreads) xs[i] = 0ull;
+      __syncthreads();
+      for (int size = 2; size <= n2; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          for (int i = tid; i < (n2 >> 1); i += kGenThreads) {
+            const int lo = 2 * i - (i & (stride - 1));
+            const int hi = lo + stride;
+            const bool desc = (lo & size) == 0;
+            const uint64_t x = xs[lo], y = xs[hi];
+            if ((x < y) == desc) {
+              xs[lo] = y;
+              xs[hi] = x;
+            }
+          }
+          __syncthreads();
+        }
+      }
+      // src/sampler.cpp:79-83: numerators of the top-k prefix, in sorted order
+      const int k = top_k_of(P, V);
+      const float mx = comp_val(xs[0]);
+      for (int j = tid; j < k; j += kGenThreads) pr[j] = numer(comp_val(xs[j]), mx, P.temp);
+      __syncthreads();
+      if (tid == 0) {
+        double sum = 0.0;  // src/sampler.cpp:84
+        for (int j = 0; j < k; ++j) sum += pr[j];
+        int keep = k;  // src/sampler.cpp:86-91
+        if (P.min_p > 0.0f) {
+          const double thr = pr[0] * static_cast<double>(P.min_p);
+          keep = 1;
+          while (keep < k && pr[keep] >= thr) ++keep;
+        }
+        const int keep_minp = keep;
+        if (P.top_p > 0.0f && P.top_p < 1.0f) {  // src/sampler.cpp:92-100
+          const double tp = static_cast<double>(P.top_p);
+          double acc = 0.0;
+          int i = 0;
+          for (; i < keep; ++i) {
+            acc += pr[i] / sum;
+            if (acc >= tp) break;
+          }
+          if (i + 1 < keep) keep = i + 1;
+        }
+        double tot = 0.0;  // src/sampler.cpp:101-108
+        for (int j = 0; j < keep; ++j) tot += pr[j];
+        const double u = a.x_u[row];
+        double r = u * tot, before = r;
+        int pick = keep - 1;
+        bool picked = false;
+        for (int j = 0; j < keep; ++j) {
+          before = r;
+          r -= pr[j];
+          if (r <= 0.0) {
+            pick = j;
+            picked = true;
+            break;
+          }
+        }
+        double mg = fabs(r);
+        if (picked && pick > 0 && before < mg) mg = before;
+        const int id = comp_idx(xs[pick]);
+        a.out[row] = id;
+        if (a.info) {
+          vsmp_row_info inf = a.info[row];
+          inf.id = id;
+          inf.keep_minp = keep_minp;
+          inf.keep = keep;
+          inf.rank = pick;
+          inf.last_id = comp_idx(xs[keep - 1]);
+          inf.sum = sum;
+          inf.tot = tot;
+          inf.draw_margin = tot > 0.0 ? mg / tot : 0.0;
+          inf.flags = (inf.flags & ~VSMP_FLAG_DRAW_NEAR) | VSMP_FLAG_SEQ_CUTS |
+                      (inf.draw_margin < kNearDraw ? VSMP_FLAG_DRAW_NEAR : 0);
+          a.info[row] = inf;
+        }
+      }
+      __syncthreads();  // the slot and the bitmap are reused by the next row
+    }
+    __syncthreads();  // the list is refilled for the next rows
   }
 }
 
@@ -3133,6 +3277,18 @@ void launch_rows(const KArgs& a, hipStream_t st) {
     configured = true;
   }
   hipLaunchKernelGGL(k_rows, dim3(a.B), dim3(kRowNT), dyn, st, a);
+}
+
+void launch_general_exact(const KArgs& a, hipStream_t st) {
+  const size_t bytes = static_cast<size_t>(a.words) * sizeof(uint32_t);
+  const size_t dyn = (a.hist_off != nullptr && a.gen_fused && bytes <= kGenBitsLds) ? bytes : 0;
+  static bool configured = false;
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_general_exact),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGenBitsLds));
+    configured = true;
+  }
+  hipLaunchKernelGGL(k_general_exact, dim3(std::min(a.B, kExactSlots)), dim3(kGenThreads), dyn, st, a);
 }
 
 void launch_general(const KArgs& a, hipStream_t st) {
