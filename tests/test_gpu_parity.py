@@ -300,6 +300,32 @@ def test_general_path_pass_plans(ctx, mode, kind):
         assert gen.any() and (~gen).any()
 
 
+def test_general_path_top_p_ties_exact(ctx, mode):
+    """Rows of tied logits whose top-p running sum meets top_p at rounding distance: the general
+    path's bucket-order sums cannot decide such a cut, so the row is redone in the reference's
+    order and sequential sums (k_general_exact). Keep counts and ids equal the oracle's exactly, and
+    the redone rows carry VSMP_FLAG_SEQ_CUTS. The logits are all 0, which the penalty leaves as
+    they are, so that the rows with a penalised history (half of them) stay tied as well."""
+    rng = np.random.default_rng(61)
+    for Vv in (4098, 20000, 49152):
+        B = 4
+        lg = np.zeros((B, Vv), np.float32)
+        p = V.params_array(n=B, temp=1.0, top_k=0, top_p=0.5, min_p=0.0, repeat=1.0, repeat_last=0, seed=7)
+        p["top_p"] = [0.5, 0.25, 0.75, 0.5]
+        p["repeat"] = [1.0, 1.1, 1.0, 1.1]
+        p["seed"] = rng.integers(1, 1 << 62, B)
+        h, off = csr([list(rng.integers(0, Vv, 100)) if r % 2 else [] for r in range(B)])
+        log("top-p ties", mode, Vv)
+        run = Run(ctx, lg, p, h, off, cand_cap=0)
+        run.report()
+        for r in range(B):
+            o, g = run.o_info[r], run.info[r]
+            assert int(g["keep"]) == int(o["keep"]), (Vv, r, int(g["keep"]), int(o["keep"]))
+            assert run.ids[r] == run.o_ids[r], (Vv, r, run.ids[r], run.o_ids[r])
+            if o["topp_margin"] < 1e-11:
+                assert int(g["flags"]) & V.FLAG_SEQ_CUTS, (Vv, r, int(g["flags"]))
+
+
 def test_general_path_exp_accuracy(ctx):
     """The general path's fp64 exp (a 64-entry table method) against exp in long double: within
     1.01 ulp over [-745, 0] (the reference's libm exp is within one ulp too), exactly 1 at 0 and 0
