@@ -14,7 +14,7 @@
 //  k_greedy_split  a greedy batch of at most half as many rows as CUs: each row cut into parts
 //            over several CUs; the part that takes the row's last device-scope ticket writes the
 //            id (every cross-workgroup value travels in a device-scope atomic).
-//  k_topk_split  the same for a small-k batch of at most 8 long rows: each part selects its exact
+//  k_topk_split  the same for a small-k batch of at most 24 long rows: each part selects its exact
 //            top-k; the last part merges the parts' lists and runs the epilogue.
 //  k_stage1  larger vocabularies (V > 2^19), grid = rows x slices. Each workgroup loads one slice
 //            of one row into registers (the single HBM pass), applies the penalty and writes its
@@ -22,7 +22,10 @@
 //  k_finish  one workgroup per greedy / small-k row after k_stage1: merges the slice results and
 //            runs the epilogue.
 //  k_general one workgroup per remaining row (k > 256 or top-k off): a mass histogram of the fp64
-//            numerators, then count and mass selects over the row, with histograms in LDS.
+//            numerators, then count and mass selects over the row, with histograms in LDS. In row
+//            mode it takes the row's maximum pass and penalty bitmap itself.
+//  k_general_exact  after k_general: the rows it marked (a top-p cut at rounding distance of
+//            top_p) redone in the reference's order and sequential sums.
 //  k_read_probe  a plain streaming read, for the attainable-bandwidth measurement.
 //  k_exp_probe   the general path's fp64 exp over an array, for measuring its accuracy.
 #include <algorithm>
