@@ -304,8 +304,10 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
       !grow(ctx->s_max, ctx->n_max, slots, false, "scratch") || !grow(ctx->s_min, ctx->n_min, slots, false, "scratch"))
     return -1;
   if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch")) return -1;
-  // general rows marked near a top-p tie are redone exactly (rows up to kExactMaxVocab)
-  const bool exact = pl.any_general && V <= kExactMaxVocab;
+  // general rows marked near a top-p tie are redone exactly (rows up to kExactMaxVocab); shared
+  // parameters without a top-p cut mark none
+  const bool exact = pl.any_general && V <= kExactMaxVocab &&
+                     (params_per_row || (params->top_p > 0.0f && params->top_p < 1.0f));
   int x_n = 1;
   while (x_n < V) x_n <<= 1;
   if (exact && (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch") ||
