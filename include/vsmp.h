@@ -57,7 +57,7 @@ typedef struct {
   int last_id;   /* id of the last candidate of the draw set */
   int flags;     /* VSMP_FLAG_* */
   float mx;      /* largest penalised logit */
-  int n_pen;     /* distinct in-range history ids penalised (small-k and greedy paths) */
+  int n_pen;     /* distinct in-range history ids penalised */
   double sum;    /* sum of the fp64 numerators over the top-k prefix */
   double tot;    /* sum over the draw set */
   double u;      /* the uniform draw used (0 for greedy) */
@@ -77,6 +77,26 @@ typedef struct {
                                      pass over the row (the cut's bucket bounded the draw's) */
 #define VSMP_FLAG_MINP_PREFIX 128u /* general path: the min-p prefix was collected whole in one
                                       pass, and the cut and the draw taken on its sorted sums */
+
+/* Optional diagnostic outputs of a batched pick (every pointer may be NULL; device arrays).
+ * They expose the intermediate sets of src/sampler.cpp:53-108 so that callers can check them
+ * against the reference element by element. Asking for them costs extra work per row.
+ *   info:     vsmp_row_info[B].
+ *   cand_ids, cand_pr, cand_cap: [B][cand_cap]: the first min(keep, cand_cap) ids of the draw set
+ *             in the reference's sorted order (value desc, index asc) and their fp64 numerators,
+ *             for every sampled row (greedy rows draw nothing and leave them untouched, as do
+ *             entries past min(keep, cand_cap)). cand_cap <= 1024.
+ *   pen_bits: uint32[B][ceil(V/32)]: bit (i % 32) of word i / 32 of row r is set iff logit i of
+ *             row r was penalised (a distinct in-range id of the row's history window,
+ *             src/sampler.cpp:53-65); all zero for a row without penalty (repeat == 1 or no
+ *             history). Written whole by the call. */
+typedef struct {
+  vsmp_row_info* info;
+  int* cand_ids;
+  double* cand_pr;
+  int cand_cap;
+  unsigned int* pen_bits;
+} vsmp_debug;
 
 typedef struct vsmp_ctx vsmp_ctx;
 
@@ -101,18 +121,15 @@ VSMP_API void vsmp_ctx_free(vsmp_ctx* ctx);
  *       hist_off[r+1]), hist_off has B+1 entries); both NULL for no history. The window
  *       (repeat_last) and de-duplication rules are the reference's (src/sampler.cpp:53-65).
  *   u_mode/u/rng_state/counter: see vsmp_u_mode (unused pointers may be NULL).
- *   out: device int[B] picked ids. info: optional device vsmp_row_info[B].
- *   cand_ids/cand_pr/cand_cap: optional device arrays [B][cand_cap]: the first min(keep,
- *       cand_cap) draw-set ids in sorted order and their fp64 numerators (small-k path only;
- *       rows on the other paths leave them untouched).
+ *   out: device int[B] picked ids.
+ *   dbg: optional diagnostic outputs (HOST pointer to a vsmp_debug, or NULL).
  * Calls that share a context must be issued from one host thread; calls on different streams
  * with one context must not overlap. Returns 0, or -1 (bad arguments, HIP error). */
 VSMP_API int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
                              const vsmp_params* params, int params_per_row, const int* hist,
                              const int* hist_off, int u_mode, const double* u,
                              unsigned long long* rng_state, unsigned long long counter, int* out,
-                             vsmp_row_info* info, int* cand_ids, double* cand_pr, int cand_cap,
-                             void* stream);
+                             const vsmp_debug* dbg, void* stream);
 
 /* One pick on a HOST logits row with a host history and a supplied draw u: the computation of
  * verbo::Sampler::pick(logits, n) (reference src/sampler.cpp:50-109) for a sampler whose history

@@ -44,6 +44,8 @@ class Info(ctypes.Structure):
         ("n_pen", ctypes.c_int),
         ("mx", ctypes.c_float),
         ("rank", ctypes.c_int),
+        ("last_id", ctypes.c_int),
+        ("reserved", ctypes.c_int),
         ("sum", ctypes.c_double),
         ("tot", ctypes.c_double),
         ("u", ctypes.c_double),
@@ -55,7 +57,7 @@ class Info(ctypes.Structure):
 
 INFO_DTYPE = np.dtype([(n, np.dtype(t)) for n, t in [
     ("id", "i4"), ("greedy", "i4"), ("k", "i4"), ("keep_minp", "i4"), ("keep", "i4"), ("n_pen", "i4"),
-    ("mx", "f4"), ("rank", "i4"), ("sum", "f8"), ("tot", "f8"), ("u", "f8"), ("minp_margin", "f8"),
+    ("mx", "f4"), ("rank", "i4"), ("last_id", "i4"), ("reserved", "i4"), ("sum", "f8"), ("tot", "f8"), ("u", "f8"), ("minp_margin", "f8"),
     ("topp_margin", "f8"), ("draw_margin", "f8")]])
 assert INFO_DTYPE.itemsize == ctypes.sizeof(Info)
 
@@ -100,7 +102,7 @@ def load_oracle():
                                 ctypes.POINTER(Info), _P, _P, ctypes.c_int, _P, ctypes.c_int]
         lib.vo_pick_rows.restype = ctypes.c_int
         lib.vo_pick_rows.argtypes = [_P, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, _P, ctypes.c_int, _P, _P,
-                                     _P, _P, _P, _P, _P, ctypes.c_int, ctypes.c_int]
+                                     _P, _P, _P, _P, _P, ctypes.c_int, _P, ctypes.c_int, ctypes.c_int]
         lib.vo_sampler_run.restype = ctypes.c_int
         lib.vo_sampler_run.argtypes = [_P, ctypes.c_int, ctypes.POINTER(Sampling), _P, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_int, _P]
@@ -185,9 +187,10 @@ def pick(logits, cfg, hist=(), u=0.0, cand_cap=0, pen_cap=0):
     return rid, info, cand[:m].copy(), cpr[:m].copy(), pen[:min(info.n_pen, pen_cap)].copy()
 
 
-def pick_rows(logits, params, hist=None, hist_off=None, u=None, cand_cap=0, threads=None):
+def pick_rows(logits, params, hist=None, hist_off=None, u=None, cand_cap=0, threads=None, pen_cap=0):
     """Oracle picks for B rows. params: SAMPLING_DTYPE array of 1 (shared) or B entries.
-    Returns (ids, infos (INFO_DTYPE), cand [B, cand_cap], cand_pr [B, cand_cap])."""
+    Returns (ids, infos (INFO_DTYPE), cand [B, cand_cap], cand_pr [B, cand_cap]), and with
+    pen_cap > 0 a fifth item: per row, the first pen_cap penalised ids (ascending, int32 arrays)."""
     lib = load_oracle()
     lg = np.ascontiguousarray(logits, dtype=np.float32)
     B, V = lg.shape
@@ -202,10 +205,13 @@ def pick_rows(logits, params, hist=None, hist_off=None, u=None, cand_cap=0, thre
     infos = np.zeros(B, dtype=INFO_DTYPE)
     cand = np.zeros((B, max(cand_cap, 1)), dtype=np.int32) if cand_cap else None
     cpr = np.zeros((B, max(cand_cap, 1)), dtype=np.float64) if cand_cap else None
+    pen = np.zeros((B, pen_cap), dtype=np.int32) if pen_cap else None
     threads = threads or min(8, os.cpu_count() or 1)
     lib.vo_pick_rows(_ptr(lg), B, V, V, _ptr(params), per_row, _ptr(h), _ptr(ho), _ptr(uu), _ptr(out),
-                     _ptr(infos), _ptr(cand), _ptr(cpr), cand_cap, threads)
-    return out, infos, cand, cpr
+                     _ptr(infos), _ptr(cand), _ptr(cpr), cand_cap, _ptr(pen), pen_cap, threads)
+    if not pen_cap:
+        return out, infos, cand, cpr
+    return out, infos, cand, cpr, [pen[r, :min(int(infos["n_pen"][r]), pen_cap)].copy() for r in range(B)]
 
 
 def sampler_run(logits, cfg, hist=(), n_picks=1, accept_each=False):

@@ -155,6 +155,7 @@ int vo_pick(const float* logits, int n, const vo_sampling* cfg, const int* hist,
     inf.id = buf[best].i;
     inf.greedy = 1;
     inf.mx = buf[best].v;
+    inf.last_id = inf.id;
     inf.k = inf.keep_minp = inf.keep = 1;
     free(buf);
     if (info) *info = inf;
@@ -233,6 +234,7 @@ int vo_pick(const float* logits, int n, const vo_sampling* cfg, const int* hist,
     inf.draw_margin = tot > 0.0 ? mg / tot : 0.0;
   }
   inf.id = buf[pick].i;
+  inf.last_id = buf[keep - 1].i;
   inf.rank = pick;
   inf.k = k;
   inf.keep = keep;
@@ -267,6 +269,8 @@ typedef struct {
   int* cand;
   double* cand_pr;
   int cand_cap;
+  int* pen;
+  int pen_cap;
   int r0, r1;
 } rows_job;
 
@@ -281,16 +285,18 @@ static void* rows_worker(void* p) {
       H = j->hist_off[r + 1] - j->hist_off[r];
     }
     const size_t cc = (size_t)j->cand_cap * (size_t)r;
+    const size_t pc = (size_t)j->pen_cap * (size_t)r;
     j->out[r] = vo_pick(j->logits + (size_t)r * (size_t)j->ld, j->V, c, h, H, j->u ? j->u[r] : 0.0,
                         j->infos ? &j->infos[r] : NULL, j->cand ? j->cand + cc : NULL,
-                        j->cand_pr ? j->cand_pr + cc : NULL, j->cand_cap, NULL, 0);
+                        j->cand_pr ? j->cand_pr + cc : NULL, j->cand_cap, j->pen ? j->pen + pc : NULL,
+                        j->pen ? j->pen_cap : 0);
   }
   return NULL;
 }
 
 int vo_pick_rows(const float* logits, int B, int V, long long ld, const vo_sampling* params, int per_row,
                  const int* hist, const int* hist_off, const double* u, int* out, vo_info* infos,
-                 int* cand, double* cand_pr, int cand_cap, int threads) {
+                 int* cand, double* cand_pr, int cand_cap, int* pen, int pen_cap, int threads) {
   if (threads < 1) threads = 1;
   if (threads > B) threads = B > 0 ? B : 1;
   rows_job jobs[256];
@@ -298,7 +304,7 @@ int vo_pick_rows(const float* logits, int B, int V, long long ld, const vo_sampl
   if (threads > 256) threads = 256;
   for (int t = 0; t < threads; ++t) {
     rows_job j = {logits, B, V, ld, params, per_row, hist, hist_off, u, out, infos, cand, cand_pr, cand_cap,
-                  (int)((long long)B * t / threads), (int)((long long)B * (t + 1) / threads)};
+                  pen, pen_cap, (int)((long long)B * t / threads), (int)((long long)B * (t + 1) / threads)};
     jobs[t] = j;
   }
   if (threads == 1) {

@@ -39,6 +39,8 @@ typedef struct {
   int n_pen;       /* distinct in-range ids penalised */
   float mx;        /* largest penalised logit */
   int rank;        /* sorted position of the picked id (-1 for greedy) */
+  int last_id;     /* id of the draw set's last element in sorted order (the pick for greedy) */
+  int reserved;
   double sum;      /* sum of pr over the top-k prefix */
   double tot;      /* sum of pr over the draw set */
   double u;        /* uniform draw used */
@@ -72,10 +74,11 @@ int vo_pick(const float* logits, int n, const vo_sampling* cfg, const int* hist,
 
 /* B independent picks: row r uses logits + r*ld, params[per_row ? r : 0], history
  * hist[hist_off[r] .. hist_off[r+1]) (hist may be NULL) and u[r]. Rows are split over
- * `threads` pthreads. infos / cand (cand_cap per row) / cand_pr may be NULL. Returns 0. */
+ * `threads` pthreads. infos / cand (cand_cap per row) / cand_pr / pen (pen_cap per row: the
+ * row's first pen_cap penalised ids, ascending) may be NULL. Returns 0. */
 int vo_pick_rows(const float* logits, int B, int V, long long ld, const vo_sampling* params, int per_row,
                  const int* hist, const int* hist_off, const double* u, int* out, vo_info* infos,
-                 int* cand, double* cand_pr, int cand_cap, int threads);
+                 int* cand, double* cand_pr, int cand_cap, int* pen, int pen_cap, int threads);
 
 /* A reference Sampler run: seed (nonzero unless temp <= 0), accept hist[0..H), then n_picks picks on the same
  * logits, drawing u from the xorshift stream; if accept_each, each picked id is accepted before

@@ -1,13 +1,18 @@
 """Shared test helpers: run the HIP sampler through the C ABI and the oracle on the same inputs,
 then compare with the reference's tolerance rules.
 
-Comparison rules (the parity bar):
-- greedy ids, penalised sets, top-k/min-p/top-p candidate sets: bit-exact, except where the
-  oracle's own decision margin is below rounding distance (|acc - top_p| < 1e-11,
-  |pr - thr| / thr < 1e-13), which are counted;
+Comparison rules (the parity bar), applied to every row:
+- greedy ids, the penalised-index set (the kernels' own bitmaps), the largest penalised logit, k,
+  the min-p and top-p keep counts, the draw set's last id and its first cand_cap ids in sorted
+  order: bit-exact. The only exemption: a row the kernel itself flags as a min-p or top-p decision
+  at rounding distance (VSMP_FLAG_MINP_NEAR / VSMP_FLAG_TOPP_NEAR) without having redone it in
+  the reference's sequential order (VSMP_FLAG_SEQ_CUTS), where the oracle's margin is also below
+  rounding distance (|acc - top_p| < 1e-11, |pr - thr| / thr < 1e-13); such rows are counted.
 - probabilities (fp64 numerators, sums): within 1e-5 relative;
-- sampled ids: equal unless the draw lies within 1e-6 (relative) of a CDF boundary, counted.
+- sampled ids: equal, except where the draw lies within 1e-6 (relative) of a CDF boundary, or on
+  an exempt row; those are counted, and the tests require the mismatches among them to be zero.
 """
+import os
 import sys
 
 import numpy as np
@@ -26,6 +31,25 @@ def log(*a):
     sys.stdout.flush()
 
 
+_CTX = {}
+
+
+def mode_ctx(mode=None):
+    """A context created under VSMP_MODE=mode (None: the planner's choice), cached per mode: the
+    library reads its tuning switches once, when a context is created."""
+    if mode not in _CTX:
+        old = os.environ.pop("VSMP_MODE", None)
+        try:
+            if mode:
+                os.environ["VSMP_MODE"] = mode
+            _CTX[mode] = V.Context(0)
+        finally:
+            os.environ.pop("VSMP_MODE", None)
+            if old is not None:
+                os.environ["VSMP_MODE"] = old
+    return _CTX[mode]
+
+
 def csr(hists):
     off = np.zeros(len(hists) + 1, np.int32)
     off[1:] = np.cumsum([len(h) for h in hists])
@@ -36,7 +60,7 @@ def csr(hists):
 class Run:
     """One batched GPU pick and the oracle's answer on the same inputs."""
 
-    def __init__(self, ctx, logits, params, hist=None, hist_off=None, u=None, cand_cap=0, ld=None, device="cuda"):
+    def __init__(self, ctx, logits, params, hist=None, hist_off=None, u=None, cand_cap=128, ld=None, device="cuda"):
         import torch
 
         self.logits = np.ascontiguousarray(logits, np.float32)
@@ -61,63 +85,88 @@ class Run:
         if cand_cap:
             cid = torch.full((B, cand_cap), -1, dtype=torch.int32, device=device)
             cpr = torch.zeros((B, cand_cap), dtype=torch.float64, device=device)
+        # garbage in the bitmaps: the call must write them whole
+        pen = torch.full((B, (Vv + 31) // 32), -1, dtype=torch.int32, device=device)
         pr = V.Params(*[self.params[0][f].item() for f in V.SAMPLING_DTYPE.names]) if not per_row else \
             V.to_device_params(self.params, device)
-        out = ctx.pick_batch(_rows_view(dl), pr, dh, dho, V.U_SUPPLIED, du, info=info, cand_ids=cid, cand_pr=cpr)
+        out = ctx.pick_batch(_rows_view(dl), pr, dh, dho, V.U_SUPPLIED, du, info=info, cand_ids=cid, cand_pr=cpr,
+                             pen_bits=pen)
         torch.cuda.synchronize()
         self.ids = out.cpu().numpy()
         self.info = V.row_info(info)
         self.cand = cid.cpu().numpy() if cid is not None else None
         self.cand_pr = cpr.cpu().numpy() if cpr is not None else None
         self.cand_cap = cand_cap
-        self.o_ids, self.o_info, self.o_cand, self.o_pr = O.pick_rows(self.logits, self.params, hist, hist_off,
-                                                                      self.u, cand_cap=cand_cap)
+        self.pen = V.pen_ids(pen.cpu().numpy(), Vv)
+        hmax = int(np.max(np.diff(hist_off))) if hist_off is not None and len(hist_off) > 1 else 0
+        (self.o_ids, self.o_info, self.o_cand, self.o_pr,
+         self.o_pen) = O.pick_rows(self.logits, self.params, hist, hist_off, self.u, cand_cap=cand_cap,
+                                   pen_cap=max(hmax, 1))
+        self.counts = {}
 
     def report(self):
-        """Checks every row; returns (n_near_draw, n_mismatch_near) and raises on real mismatches."""
+        """Checks every row; returns (n_near_draw, n_mismatch_near) and raises on any other
+        difference. self.counts: rows per category (near draws, exempt rows, sequential redos)."""
         gi, oi = self.info, self.o_info
         problems = []
-        near = 0
-        near_mismatch = 0
+        near = exempt = seq = near_mismatch = 0
         for r in range(self.B):
             o = oi[r]
             g = gi[r]
-            set_amb = o["topp_margin"] < NEAR_TOPP or o["minp_margin"] < NEAR_MINP
-            draw_amb = o["draw_margin"] < NEAR_DRAW
-            near += int(draw_amb)
+            gf = int(g["flags"])
+            if not np.array_equal(self.pen[r], self.o_pen[r]):
+                problems.append(f"row {r}: penalised ids differ ({len(self.pen[r])} vs {len(self.o_pen[r])})")
+            if g["n_pen"] != o["n_pen"]:
+                problems.append(f"row {r}: n_pen {g['n_pen']} != {o['n_pen']}")
             if g["id"] != self.ids[r]:
                 problems.append(f"row {r}: out {self.ids[r]} != info.id {g['id']}")
-            if g["flags"] & V.FLAG_CUTS_DIFFER:
+            if gf & V.FLAG_CUTS_DIFFER:
                 problems.append(f"row {r}: parallel and sequential cuts differ")
+            if not np.float32(g["mx"]) == np.float32(o["mx"]):
+                problems.append(f"row {r}: mx {g['mx']} != {o['mx']}")
             if o["greedy"]:
                 if self.ids[r] != self.o_ids[r]:
                     problems.append(f"row {r}: greedy id {self.ids[r]} != oracle {self.o_ids[r]}")
                 continue
+            near_o = o["topp_margin"] < NEAR_TOPP or o["minp_margin"] < NEAR_MINP
+            flagged = gf & (V.FLAG_TOPP_NEAR | V.FLAG_MINP_NEAR)
+            redone = gf & V.FLAG_SEQ_CUTS
+            set_amb = bool(near_o and flagged and not redone)
+            exempt += int(set_amb)
+            seq += int(bool(redone))
+            draw_amb = o["draw_margin"] < NEAR_DRAW
+            near += int(draw_amb)
             if g["k"] != o["k"]:
                 problems.append(f"row {r}: k {g['k']} != {o['k']}")
-            if not set_amb and (g["keep_minp"] != o["keep_minp"] or g["keep"] != o["keep"]):
-                problems.append(f"row {r}: keep ({g['keep_minp']},{g['keep']}) != ({o['keep_minp']},{o['keep']})")
-            if not np.float32(g["mx"]) == np.float32(o["mx"]):
-                problems.append(f"row {r}: mx {g['mx']} != {o['mx']}")
+            if not set_amb:
+                if g["keep_minp"] != o["keep_minp"] or g["keep"] != o["keep"]:
+                    problems.append(f"row {r}: keep ({g['keep_minp']},{g['keep']}) != ({o['keep_minp']},{o['keep']})")
+                if g["last_id"] != o["last_id"]:
+                    problems.append(f"row {r}: last id of the draw set {g['last_id']} != {o['last_id']}")
+                if abs(g["tot"] - o["tot"]) > PROB_RTOL * abs(o["tot"]):
+                    problems.append(f"row {r}: tot {g['tot']} vs {o['tot']}")
             if abs(g["sum"] - o["sum"]) > PROB_RTOL * abs(o["sum"]):
                 problems.append(f"row {r}: sum {g['sum']} vs {o['sum']}")
-            if not set_amb and abs(g["tot"] - o["tot"]) > PROB_RTOL * abs(o["tot"]):
-                problems.append(f"row {r}: tot {g['tot']} vs {o['tot']}")
             if self.ids[r] != self.o_ids[r]:
                 if draw_amb or set_amb:
                     near_mismatch += 1
                 else:
                     problems.append(f"row {r}: id {self.ids[r]} != oracle {self.o_ids[r]} "
-                                    f"(draw margin {o['draw_margin']:.3g}, keep {o['keep']})")
-            if self.cand is not None and g["path"] == V.PATH_SMALLK and not set_amb:
+                                    f"(draw margin {o['draw_margin']:.3g}, keep {o['keep']}, path {g['path']})")
+            if self.cand is not None and not set_amb:
                 m = min(int(o["keep"]), self.cand_cap)
                 if not (self.cand[r, :m] == self.o_cand[r, :m]).all():
-                    problems.append(f"row {r}: candidate ids differ")
+                    bad = int(np.argmax(self.cand[r, :m] != self.o_cand[r, :m]))
+                    problems.append(f"row {r}: candidate ids differ from position {bad} of {m} (path {g['path']})")
+                if self.cand_cap > m and (self.cand[r, m:] != -1).any():
+                    problems.append(f"row {r}: candidate ids written past min(keep, cand_cap)")
                 p, q = self.cand_pr[r, :m], self.o_pr[r, :m]
                 if (np.abs(p - q) > PROB_RTOL * np.abs(q)).any():
                     problems.append(f"row {r}: candidate probabilities differ by {np.max(np.abs(p - q) / q):.3g}")
         if problems:
             raise AssertionError(f"{len(problems)} problems:\n" + "\n".join(problems[:20]))
+        self.counts = {"rows": self.B, "near_draws": near, "exempt_rows": exempt, "sequential_redos": seq,
+                       "mismatches_near": near_mismatch}
         return near, near_mismatch
 
 

@@ -9,7 +9,7 @@ import pytest
 
 import oracle as O
 import verbo_amd as V
-from helpers import Run, csr, log
+from helpers import Run, csr, log, mode_ctx
 from verbo_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -18,20 +18,21 @@ KAT = np.array([0.1, 3.0, 2.9, -1.0, 0.0], np.float32)
 
 
 @pytest.fixture(params=["slices", "rows", "split"])
-def mode(request, monkeypatch):
+def mode(request):
     """Each decomposition on the same inputs: slices + merge, one workgroup per row, and (for
-    greedy batches with shared parameters; other batches take the default) rows cut into parts
-    finished by their last part. The library reads VSMP_MODE on every call."""
-    monkeypatch.setenv("VSMP_MODE", request.param)
+    greedy and small-k batches with shared parameters; other batches take the default) rows cut
+    into parts finished by their last part. A context reads VSMP_MODE when it is created."""
     return request.param
 
 
-@pytest.fixture(scope="module")
-def ctx():
+@pytest.fixture
+def ctx(request):
+    """A context in the test's decomposition mode (the planner's choice when it has none)."""
     import torch
 
     assert torch.cuda.is_available(), "the gpu tests need a ROCm device"
-    return V.Context(0)
+    m = request.getfixturevalue("mode") if "mode" in request.fixturenames else None
+    return mode_ctx(m)
 
 
 def test_reference_kats_on_gpu():
@@ -153,17 +154,22 @@ def test_no_history_and_padded_rows(ctx, mode):
 def test_workloads_reduced(ctx, mode, name):
     w = W.make(name, rows=32)
     log("workload", mode, name, w.B, w.V)
-    n, nm = Run(ctx, w.logits, w.params, w.hist, w.hist_off, cand_cap=256).report()
-    log(f"  near-boundary draws {n}, mismatches among them {nm}")
+    run = Run(ctx, w.logits, w.params, w.hist, w.hist_off, cand_cap=256)
+    n, nm = run.report()
+    log(f"  {run.counts}")
+    assert nm == 0
 
 
 @pytest.mark.parametrize("name", ["greedy", "peaked", "wide", "mixed"])
 def test_workloads_full_size(ctx, name):
+    """Every row of the four batched workloads at full size, every diagnostic compared; the
+    draws within 1e-6 of a CDF boundary are counted and must still pick the oracle's id."""
     w = W.make(name)
     log("workload full", name, w.B, w.V)
-    n, nm = Run(ctx, w.logits, w.params, w.hist, w.hist_off, cand_cap=128).report()
-    log(f"  near-boundary draws {n} of {w.B}, mismatches among them {nm}")
-    assert nm <= max(1, n // 10)
+    run = Run(ctx, w.logits, w.params, w.hist, w.hist_off, cand_cap=128)
+    n, nm = run.report()
+    log(f"  {run.counts}")
+    assert nm == 0
 
 
 def test_draw_modes(ctx, mode):
@@ -316,7 +322,7 @@ def test_general_path_top_p_ties_exact(ctx, mode):
         p["seed"] = rng.integers(1, 1 << 62, B)
         h, off = csr([list(rng.integers(0, Vv, 100)) if r % 2 else [] for r in range(B)])
         log("top-p ties", mode, Vv)
-        run = Run(ctx, lg, p, h, off, cand_cap=0)
+        run = Run(ctx, lg, p, h, off, cand_cap=128)
         run.report()
         for r in range(B):
             o, g = run.o_info[r], run.info[r]
@@ -348,14 +354,14 @@ def test_general_path_exp_accuracy(ctx):
 
 
 @pytest.mark.parametrize("dmode", ["split", "rows"])
-def test_greedy_split_parts(ctx, monkeypatch, dmode):
+def test_greedy_split_parts(dmode):
     """Greedy batches cut into parts (one launch, the last part of a row writes its id) against the
     oracle and against one workgroup per row: ties of the maximum in different parts (the lowest
     index wins), the maximum itself penalised, parts that end inside a 16-byte group or hold no
     group, consecutive calls reusing the per-row slots, and a call without diagnostics."""
     import torch
 
-    monkeypatch.setenv("VSMP_MODE", dmode)
+    ctx = mode_ctx(dmode)
     rng = np.random.default_rng(31)
     for B, Vv in [(1, 49152), (3, 1001), (5, 4097), (2, 20001), (17, 151936), (9, 131075), (40, 2052)]:
         lg = rng.normal(0, 3, (B, Vv)).astype(np.float32)
@@ -468,7 +474,7 @@ def test_graph_capture_and_replay(ctx):
 
 
 @pytest.mark.parametrize("dmode", ["split", "rows"])
-def test_topk_split_parts(ctx, monkeypatch, dmode):
+def test_topk_split_parts(dmode):
     """Small-k batches cut into parts (one launch, the last part merges the parts' sorted lists and
     runs the epilogue) against the oracle, and row mode on the same inputs: ties of the largest
     values in different parts, penalised candidates, k from 1 to 256, min-p and top-p, parts that
@@ -476,7 +482,7 @@ def test_topk_split_parts(ctx, monkeypatch, dmode):
     once per row), candidate lists, and consecutive calls reusing the per-row tickets."""
     import torch
 
-    monkeypatch.setenv("VSMP_MODE", dmode)
+    ctx = mode_ctx(dmode)
     rng = np.random.default_rng(61)
     for B, Vv, k in [(1, 151936, 40), (3, 49152, 1), (2, 20001, 256), (8, 131075, 50), (5, 4097, 7),
                      (1, 600_003, 100)]:

@@ -134,6 +134,37 @@ def test_topk_order_and_penalty_brute_force(oracle):
         assert g == order[0]
 
 
+def test_penalised_ids_and_last_id_brute_force(oracle):
+    """The oracle's penalised-id list (ascending distinct in-range ids of the window, none when
+    repeat == 1) and its draw set's last id, which the GPU's diagnostics are compared with, against
+    a brute force: the ids whose value the penalty changed, and the keep-th id of a full sort.
+    Batched rows (vo_pick_rows) give the same lists as single picks."""
+    rng = np.random.default_rng(13)
+    rows = []
+    for t in range(40):
+        V = 97
+        lg = (rng.normal(0, 2, V).astype(np.float32) + 0.25).astype(np.float32)
+        lg[lg == 0] = 0.5  # the penalty leaves 0 unchanged; keep every value visibly penalisable
+        hist = rng.integers(-3, V + 3, int(rng.integers(0, 80)))
+        rep = float(rng.choice([1.0, 1.3, 0.7]))
+        rl = int(rng.choice([0, 7, 64, -1]))
+        c = oracle.sampling(temp=0.9, top_k=int(rng.choice([0, 5, 30])), top_p=float(rng.choice([0.6, 1.0])),
+                            min_p=0.0, repeat=rep, repeat_last=rl, seed=1)
+        _, info, cand, _, pen = oracle.pick(lg, c, hist, u=0.4, cand_cap=V, pen_cap=V)
+        changed = np.flatnonzero(_penalised(lg, hist, np.float32(rep), rl) != lg)
+        assert pen.tolist() == changed.tolist() and info.n_pen == changed.size, t
+        order = _sorted_ids(_penalised(lg, hist, np.float32(rep), rl))
+        assert info.last_id == order[info.keep - 1] == cand[info.keep - 1]
+        rows.append((lg, c, hist, pen, info.last_id))
+    lg = np.stack([r[0] for r in rows])
+    params = oracle.params_array([r[1] for r in rows])
+    off = np.concatenate([[0], np.cumsum([len(r[2]) for r in rows])]).astype(np.int32)
+    flat = np.concatenate([r[2] for r in rows]).astype(np.int32)
+    _, infos, _, _, pens = oracle.pick_rows(lg, params, flat, off, np.full(len(rows), 0.4), pen_cap=97)
+    for r, row in enumerate(rows):
+        assert pens[r].tolist() == row[3].tolist() and infos["last_id"][r] == row[4]
+
+
 def test_inverse_cdf_closed_forms(oracle):
     rng = np.random.default_rng(5)
     # equal logits: the draw is ceil(u*V)-1

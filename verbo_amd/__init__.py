@@ -17,7 +17,7 @@ import numpy as np
 
 from .workloads import SAMPLING_DTYPE
 
-__all__ = ["Context", "Sampler", "Params", "RowInfo", "VsmpError", "load_library", "U_SUPPLIED", "U_COUNTER",
+__all__ = ["Context", "Sampler", "Params", "RowInfo", "Debug", "VsmpError", "load_library", "U_SUPPLIED", "U_COUNTER",
            "U_XORSHIFT", "ROW_INFO_DTYPE", "SAMPLING_DTYPE"]
 __version__ = "0.1.0"
 
@@ -69,6 +69,18 @@ class RowInfo(ctypes.Structure):
     ]
 
 
+class Debug(ctypes.Structure):
+    """vsmp_debug: optional diagnostic outputs of vsmp_pick_batch (device addresses)."""
+
+    _fields_ = [
+        ("info", ctypes.c_void_p),
+        ("cand_ids", ctypes.c_void_p),
+        ("cand_pr", ctypes.c_void_p),
+        ("cand_cap", ctypes.c_int),
+        ("pen_bits", ctypes.c_void_p),
+    ]
+
+
 ROW_INFO_DTYPE = np.dtype([("id", "i4"), ("path", "i4"), ("k", "i4"), ("keep_minp", "i4"), ("keep", "i4"),
                            ("rank", "i4"), ("last_id", "i4"), ("flags", "i4"), ("mx", "f4"), ("n_pen", "i4"),
                            ("sum", "f8"), ("tot", "f8"), ("u", "f8"), ("draw_margin", "f8")])
@@ -111,8 +123,8 @@ def load_library():
         "vsmp_ctx_new": (_P, [ctypes.c_int]),
         "vsmp_ctx_free": (None, [_P]),
         "vsmp_pick_batch": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, _P, ctypes.c_int,
-                                           _P, _P, ctypes.c_int, _P, _P, ctypes.c_ulonglong, _P, _P, _P, _P,
-                                           ctypes.c_int, _P]),
+                                           _P, _P, ctypes.c_int, _P, _P, ctypes.c_ulonglong, _P,
+                                           ctypes.POINTER(Debug), _P]),
         "vsmp_pick_host": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.POINTER(Params), _P, ctypes.c_int,
                                           ctypes.c_double, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(RowInfo)]),
         "vsmp_sampler_new": (_P, [ctypes.POINTER(Params)]),
@@ -181,6 +193,13 @@ def row_info(t):
     return t.cpu().numpy().view(ROW_INFO_DTYPE)
 
 
+def pen_ids(bits, V):
+    """Ascending penalised ids per row from a pen_bits bitmap (numpy int32 [B, ceil(V/32)])."""
+    b = np.ascontiguousarray(bits).view(np.uint32)
+    flat = np.unpackbits(b.view(np.uint8).reshape(b.shape[0], -1), axis=1, bitorder="little")[:, :V]
+    return [np.nonzero(r)[0].astype(np.int32) for r in flat]
+
+
 class Context:
     """A vsmp_ctx on one device: scratch for batched picks, staging for host picks."""
 
@@ -201,9 +220,11 @@ class Context:
         self.close()
 
     def pick_batch(self, logits, params, hist=None, hist_off=None, u_mode=U_COUNTER, u=None, rng_state=None,
-                   counter=0, out=None, info=None, cand_ids=None, cand_pr=None, stream=None):
+                   counter=0, out=None, info=None, cand_ids=None, cand_pr=None, pen_bits=None, stream=None):
         """vsmp_pick_batch on torch device tensors. `params`: a Params (shared by all rows) or a
         device byte tensor from to_device_params (one entry per row). Returns `out` (int32 [B]).
+        Diagnostics (vsmp_debug): info (uint8 [B*72]), cand_ids (int32 [B, cap]) / cand_pr (float64
+        [B, cap]), pen_bits (int32 [B, ceil(V/32)]).
         Stream-ordered on `stream` (default: torch's current stream); does not synchronise."""
         import torch
 
@@ -224,12 +245,17 @@ class Context:
         cap = 0
         if cand_ids is not None:
             cap = cand_ids.shape[1]
+        if pen_bits is not None and pen_bits.numel() != B * ((V + 31) // 32):
+            raise VsmpError("pen_bits must hold B * ceil(V / 32) words")
+        dbg = None
+        if info is not None or cand_ids is not None or pen_bits is not None:
+            dbg = Debug(_addr(info), _addr(cand_ids), _addr(cand_pr), cap, _addr(pen_bits))
         st = stream if stream is not None else torch.cuda.current_stream(logits.device)
         if not logits.is_cuda:
             raise VsmpError("logits must be a device tensor")
         rc = _lib.vsmp_pick_batch(self._h, logits.data_ptr(), B, V, ld, pp, per_row, _addr(hist), _addr(hist_off),
-                                  int(u_mode), _addr(u), _addr(rng_state), int(counter), _addr(out), _addr(info),
-                                  _addr(cand_ids), _addr(cand_pr), cap, ctypes.c_void_p(st.cuda_stream))
+                                  int(u_mode), _addr(u), _addr(rng_state), int(counter), _addr(out),
+                                  ctypes.byref(dbg) if dbg is not None else None, ctypes.c_void_p(st.cuda_stream))
         if rc != 0:
             raise _err()
         return out

@@ -34,20 +34,23 @@ bool hip_ok(hipError_t e, const char* what) {
   return false;
 }
 
+// Grows a context buffer to `need` elements. `done` is the event the context records after the last
+// work of every call (calls that share a context never overlap): the old buffer is freed once it
+// has completed, without waiting for the rest of the device.
+// A buffer that must start at zero is cleared on `zst`, the stream of the call that will use it.
 template <class T>
-bool grow(T*& p, size_t& cap, size_t need, bool zero, const char* what) {
+bool grow(T*& p, size_t& cap, size_t need, bool zero, const char* what, hipEvent_t done, hipStream_t zst = nullptr) {
   if (need <= cap && p) return true;
   size_t n = std::max<size_t>(need, cap * 2);
   if (p) {
-    // a kernel launched earlier may still read the old buffer
-    if (!hip_ok(hipDeviceSynchronize(), "synchronise before growing scratch")) return false;
+    if (!hip_ok(hipEventSynchronize(done), "wait for the last call before growing scratch")) return false;
     (void)hipFree(p);
     p = nullptr;
     cap = 0;
   }
   void* q = nullptr;
   if (!hip_ok(hipMalloc(&q, n * sizeof(T)), what)) return false;
-  if (zero && !hip_ok(hipMemset(q, 0, n * sizeof(T)), what)) {
+  if (zero && !hip_ok(hipMemsetAsync(q, 0, n * sizeof(T), zst), what)) {
     (void)hipFree(q);
     return false;
   }
@@ -68,6 +71,12 @@ int path_host(const vsmp_params& p, int V, bool smallk_ok) {
 struct vsmp_ctx {
   int device = 0;
   int cus = 256;                 // compute units of the device
+  // tuning and testing switches, read from the environment when the context is created:
+  // VSMP_MODE=rows|slices|split (-1: the planner's choice), VSMP_SPLIT_P, VSMP_EPT
+  int mode = -1;
+  long long split_p = 0;
+  int ept = 0;
+  hipEvent_t done_ev = nullptr;  // recorded after the last work of every call (see grow)
   hipStream_t stream = nullptr;  // used by the host-pointer path
   // row mode with per-row parameters: k_general runs on `side`, forked from and joined back to the
   // caller's stream by the two events, next to k_rows
@@ -134,7 +143,7 @@ struct Plan {
 // (topk_parts), else rows whenever the vocabulary fits the row kernel (V <= 2^19), slices beyond.
 // split applies to greedy and small-k batches with shared parameters only; other batches take the
 // default.
-int forced_mode() {
+int env_mode() {
   const char* e = std::getenv("VSMP_MODE");
   if (!e) return -1;
   if (std::strcmp(e, "rows") == 0) return 1;
@@ -145,17 +154,13 @@ int forced_mode() {
 
 // Parts per row of a split greedy batch: enough workgroups for two per CU, at most
 // kSplitMaxPartGroups 16-byte groups per part (all its loads in flight at once), at least 512
-// groups per part (one per thread). 0: no split.
-int split_parts(int B, int V, int cus, bool forced) {
+// groups per part (one per thread). 0: no split. forced_p (VSMP_SPLIT_P, tuning) > 0 pins the parts
+// per row within [pmin, pmax].
+int split_parts(int B, int V, int cus, bool forced, long long forced_p) {
   const long long V4 = (static_cast<long long>(V) + 3) / 4;
   const long long pmin = (V4 + kSplitMaxPartGroups - 1) / kSplitMaxPartGroups;
   const long long pcus = (2LL * cus + B - 1) / B;
   const long long pmax = std::max(pmin, V4 / 512);
-  // VSMP_SPLIT_P pins the parts per row (tuning), within [pmin, pmax]
-  static const long long forced_p = [] {
-    const char* e = std::getenv("VSMP_SPLIT_P");
-    return e ? std::atoll(e) : 0LL;
-  }();
   const long long P = forced_p > 0 ? std::min(std::max(forced_p, pmin), pmax) : std::min(std::max(pmin, pcus), pmax);
   if (!forced && (2LL * B > cus || P < 2)) return 0;
   if (static_cast<long long>(B) * P > INT32_MAX) return 0;
@@ -166,15 +171,11 @@ int split_parts(int B, int V, int cus, bool forced) {
 // (a part's cost is mostly fixed, and the last part merges one list per part), within what the last
 // part can merge: a part's list holds up to kKmax entries (all its keys above its bound, when they
 // fit), so P * kKmax <= kMergeCap. 0: no split.
-int topk_parts(int B, int V, int cus, int k, bool forced) {
+int topk_parts(int B, int V, int cus, int k, bool forced, long long forced_p) {
   const long long V4 = (static_cast<long long>(V) + 3) / 4;
   const long long pmin = (V4 + kSplitMaxPartGroups - 1) / kSplitMaxPartGroups;
   const long long pmax = std::min<long long>({std::max(pmin, V4 / 512), kMaxMergeSlices, kMergeCap / kKmax});
   if (pmin > pmax) return 0;
-  static const long long forced_p = [] {
-    const char* e = std::getenv("VSMP_SPLIT_P");
-    return e ? std::atoll(e) : 0LL;
-  }();
   const long long P = forced_p > 0 ? std::min(std::max(forced_p, pmin), pmax) : pmin;
   // Measured against row mode (top-k 40, V = 151936): faster up to B = 24 (1: 17.9 against 21.5,
   // 8: 18.6 / 22.8, 16: 20.7 / 22.6, 24: 20.5 / 23.1 us), even at 32 (22.8 / 23.0); slower at any B
@@ -187,14 +188,15 @@ int topk_parts(int B, int V, int cus, int k, bool forced) {
 
 // Slice shape: enough workgroups to fill the chip (>= 2048), slices of 256*EPT elements, and no
 // more slices than the small-k merge can hold (S * k <= kMergeCap).
-Plan plan(int B, int V, const vsmp_params* hostp, int cus) {
+Plan plan(const vsmp_ctx* ctx, int B, int V, const vsmp_params* hostp) {
   Plan pl{};
-  const int fm = forced_mode();
+  const int fm = ctx->mode;
+  const int cus = ctx->cus;
   if (hostp && (fm == -1 || fm == 2)) {
     const int path = path_host(*hostp, V, true);
     const int k = (hostp->top_k > 0 && hostp->top_k < V) ? hostp->top_k : V;
-    const int P = path == kPathGreedy ? split_parts(B, V, cus, fm == 2)
-                                      : (path == kPathSmallK ? topk_parts(B, V, cus, k, fm == 2) : 0);
+    const int P = path == kPathGreedy ? split_parts(B, V, cus, fm == 2, ctx->split_p)
+                                      : (path == kPathSmallK ? topk_parts(B, V, cus, k, fm == 2, ctx->split_p) : 0);
     if (P > 0) {
       pl.split = true;
       pl.topk = path == kPathSmallK;
@@ -249,12 +251,7 @@ Plan plan(int B, int V, const vsmp_params* hostp, int cus) {
   const bool need_merge = !uniform_path || upath == kPathSmallK;
   const int epts[3] = {64, 32, 16};
   pl.ept = 64;
-  // VSMP_EPT (16, 32 or 64) pins the elements per thread of stage 1, for tuning
-  static const int forced = [] {
-    const char* e = std::getenv("VSMP_EPT");
-    const int v = e ? std::atoi(e) : 0;
-    return (v == 16 || v == 32 || v == 64) ? v : 0;
-  }();
+  const int forced = ctx->ept;  // VSMP_EPT (16, 32 or 64) pins the elements per thread of stage 1
   for (int e : epts) {
     if (forced && e != forced) continue;
     const int L = kTpb * e;
@@ -281,10 +278,15 @@ Plan plan(int B, int V, const vsmp_params* hostp, int cus) {
   return pl;
 }
 
-int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
-               int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
-               unsigned long long* rng_state, unsigned long long counter, int* out, vsmp_row_info* info,
-               int* cand_ids, double* cand_pr, int cand_cap, hipStream_t st) {
+int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
+                 int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
+                 unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
+                 hipStream_t st) {
+  vsmp_row_info* info = dbg ? dbg->info : nullptr;
+  int* cand_ids = dbg ? dbg->cand_ids : nullptr;
+  double* cand_pr = dbg ? dbg->cand_pr : nullptr;
+  const int cand_cap = dbg ? dbg->cand_cap : 0;
+  uint32_t* pen_bits = dbg ? dbg->pen_bits : nullptr;
   if (!ctx) return set_error("vsmp: null context");
   if (!logits || !out || !params) return set_error("vsmp: logits, params and out are required");
   if (B < 1 || V < 1) return set_error("vsmp: need B >= 1 and V >= 1");
@@ -296,27 +298,36 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   if (u_mode == VSMP_U_XORSHIFT && !rng_state) return set_error("vsmp: rng_state is required with VSMP_U_XORSHIFT");
   if (u_mode < VSMP_U_SUPPLIED || u_mode > VSMP_U_XORSHIFT) return set_error("vsmp: unknown u_mode");
   if (cand_cap < 0 || (cand_cap > 0 && !cand_ids)) return set_error("vsmp: cand_ids is required with cand_cap > 0");
-  const Plan pl = plan(B, V, params_per_row ? nullptr : params, ctx->cus);
+  if (cand_cap > kGenCap) return set_error("vsmp: cand_cap is at most " + std::to_string(kGenCap));
+  const Plan pl = plan(ctx, B, V, params_per_row ? nullptr : params);
   const size_t slots = static_cast<size_t>(B) * static_cast<size_t>(pl.S);
   if (slots > static_cast<size_t>(INT32_MAX) / kKmax) return set_error("vsmp: batch too large");
   const int words = (V + 31) / 32;
-  if (!grow(ctx->s_cnt, ctx->n_cnt, slots, false, "scratch") || !grow(ctx->s_npen, ctx->n_npen, slots, false, "scratch") ||
-      !grow(ctx->s_max, ctx->n_max, slots, false, "scratch") || !grow(ctx->s_min, ctx->n_min, slots, false, "scratch"))
+  hipEvent_t busy = ctx->done_ev;
+  if (!grow(ctx->s_cnt, ctx->n_cnt, slots, false, "scratch", busy) ||
+      !grow(ctx->s_npen, ctx->n_npen, slots, false, "scratch", busy) ||
+      !grow(ctx->s_max, ctx->n_max, slots, false, "scratch", busy) ||
+      !grow(ctx->s_min, ctx->n_min, slots, false, "scratch", busy))
     return -1;
-  if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch")) return -1;
-  // general rows marked near a top-p tie are redone exactly (rows up to kExactMaxVocab); shared
-  // parameters without a top-p cut mark none
-  const bool exact = pl.any_general && V <= kExactMaxVocab &&
-                     (params_per_row || (params->top_p > 0.0f && params->top_p < 1.0f));
+  if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch", busy)) return -1;
+  // General rows marked near a top-p tie are redone exactly (rows up to kExactMaxVocab). The scratch
+  // is sized whenever a batch may hold general rows, whatever its parameters, so that one call at a
+  // shape sizes it for every later call at that shape (graph capture); the launch is skipped for
+  // shared parameters without a top-p cut, which mark no row.
+  const bool exact_scratch = pl.any_general && V <= kExactMaxVocab;
+  const bool exact = exact_scratch && (params_per_row || (params->top_p > 0.0f && params->top_p < 1.0f));
   int x_n = 1;
   while (x_n < V) x_n <<= 1;
-  if (exact && (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch") ||
-                !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch") ||
-                !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(kExactSlots) * 2 * x_n, false, "scratch")))
+  if (exact_scratch && (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch", busy) ||
+                        !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch", busy) ||
+                        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(kExactSlots) * 2 * x_n, false, "scratch", busy)))
     return -1;
-  if (pl.any_general && hist && !pl.rows &&
-      !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch"))
+  if (pl.any_general && !pl.rows && !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch", busy))
     return -1;
+  if (pen_bits) {  // diagnostics: the kernels store or OR each row's penalised ids into zeroed bitmaps
+    launch_zero_u32(pen_bits, static_cast<long long>(B) * words, st);
+    if (!hip_ok(hipGetLastError(), "zero-fill launch")) return -1;
+  }
 
   KArgs a{};
   a.logits = logits;
@@ -340,6 +351,7 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   a.cand_ids = cand_ids;
   a.cand_pr = cand_pr;
   a.cand_cap = cand_cap;
+  a.pen_bits = pen_bits;
   a.S = pl.S;
   a.L = pl.L;
   a.xcd_map = pl.xcd;
@@ -357,9 +369,9 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   a.x_buf = ctx->x_buf;
   a.x_n = x_n;
   if (pl.split) {
-    if (!grow(ctx->g_slot, ctx->n_slot, static_cast<size_t>(B), true, "scratch") ||
-        !grow(ctx->g_tick, ctx->n_tick, static_cast<size_t>(B), true, "scratch") ||
-        !grow(ctx->g_npen, ctx->n_gnpen, static_cast<size_t>(B), true, "scratch"))
+    if (!grow(ctx->g_slot, ctx->n_slot, static_cast<size_t>(B), true, "scratch", busy, st) ||
+        !grow(ctx->g_tick, ctx->n_tick, static_cast<size_t>(B), true, "scratch", busy, st) ||
+        !grow(ctx->g_npen, ctx->n_gnpen, static_cast<size_t>(B), true, "scratch", busy, st))
       return -1;
     a.P = pl.P;
     a.g_slot = ctx->g_slot;
@@ -414,6 +426,26 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
   return 0;
 }
 
+// Records the context's completion event after a call's work on `st` (not while `st` is being
+// captured into a graph: nothing runs then, and the scratch is sized before any capture).
+bool mark_done(vsmp_ctx* ctx, hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (!hip_ok(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing")) return false;
+  if (cs != hipStreamCaptureStatusNone) return true;
+  return hip_ok(hipEventRecord(ctx->done_ev, st), "hipEventRecord");
+}
+
+int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
+               int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
+               unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
+               hipStream_t st) {
+  if (!ctx) return set_error("vsmp: null context");
+  const int rc = launch_batch(ctx, logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
+                              out, dbg, st);
+  if (!mark_done(ctx, st)) return -1;
+  return rc;
+}
+
 }  // namespace
 }  // namespace vsmp
 
@@ -430,12 +462,19 @@ vsmp_ctx* vsmp_ctx_new(int device) {
   if (!vsmp::hip_ok(hipSetDevice(dev), "hipSetDevice")) return nullptr;
   vsmp_ctx* c = new vsmp_ctx();
   c->device = dev;
+  c->mode = vsmp::env_mode();
+  if (const char* e = std::getenv("VSMP_SPLIT_P")) c->split_p = std::atoll(e);
+  if (const char* e = std::getenv("VSMP_EPT")) {
+    const int v = std::atoi(e);
+    c->ept = (v == 16 || v == 32 || v == 64) ? v : 0;
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) c->cus = cus;
   if (!vsmp::hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate") ||
       !vsmp::hip_ok(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking), "hipStreamCreate") ||
       !vsmp::hip_ok(hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming), "hipEventCreate") ||
-      !vsmp::hip_ok(hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming), "hipEventCreate")) {
+      !vsmp::hip_ok(hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming), "hipEventCreate") ||
+      !vsmp::hip_ok(hipEventCreateWithFlags(&c->done_ev, hipEventDisableTiming), "hipEventCreate")) {
     vsmp_ctx_free(c);
     return nullptr;
   }
@@ -454,17 +493,18 @@ void vsmp_ctx_free(vsmp_ctx* c) {
   if (c->side) (void)hipStreamDestroy(c->side);
   if (c->fork_ev) (void)hipEventDestroy(c->fork_ev);
   if (c->join_ev) (void)hipEventDestroy(c->join_ev);
+  if (c->done_ev) (void)hipEventDestroy(c->done_ev);
   delete c;
 }
 
 int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
                     int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
-                    unsigned long long* rng_state, unsigned long long counter, int* out, vsmp_row_info* info,
-                    int* cand_ids, double* cand_pr, int cand_cap, void* stream) {
+                    unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
+                    void* stream) {
   vsmp::clear_error();
   if (ctx && !vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
   return vsmp::pick_batch(ctx, logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
-                          out, info, cand_ids, cand_pr, cand_cap, static_cast<hipStream_t>(stream));
+                          out, dbg, static_cast<hipStream_t>(stream));
 }
 
 int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params* params, const int* hist, int H,
@@ -477,12 +517,13 @@ int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params*
   if (H < 0 || (H > 0 && !hist)) return vsmp::set_error("vsmp: bad history");
   if (!hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
   const long long ld = (n + 3) & ~3;
-  if (!grow(ctx->d_logits, ctx->n_logits, static_cast<size_t>(ld), false, "host-path buffers") ||
-      !grow(ctx->d_hist, ctx->n_hist, static_cast<size_t>(std::max(H, 1)), false, "host-path buffers") ||
-      !grow(ctx->d_hoff, ctx->n_hoff, 2, false, "host-path buffers") ||
-      !grow(ctx->d_u, ctx->n_u, 1, false, "host-path buffers") ||
-      !grow(ctx->d_out, ctx->n_out, 1, false, "host-path buffers") ||
-      !grow(ctx->d_info, ctx->n_info, 1, false, "host-path buffers"))
+  hipEvent_t busy = ctx->done_ev;
+  if (!grow(ctx->d_logits, ctx->n_logits, static_cast<size_t>(ld), false, "host-path buffers", busy) ||
+      !grow(ctx->d_hist, ctx->n_hist, static_cast<size_t>(std::max(H, 1)), false, "host-path buffers", busy) ||
+      !grow(ctx->d_hoff, ctx->n_hoff, 2, false, "host-path buffers", busy) ||
+      !grow(ctx->d_u, ctx->n_u, 1, false, "host-path buffers", busy) ||
+      !grow(ctx->d_out, ctx->n_out, 1, false, "host-path buffers", busy) ||
+      !grow(ctx->d_info, ctx->n_info, 1, false, "host-path buffers", busy))
     return -1;
   hipStream_t st = ctx->stream;
   const int hoff[2] = {0, H};
@@ -493,9 +534,11 @@ int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params*
       !hip_ok(hipMemcpyAsync(ctx->d_hoff, hoff, sizeof hoff, hipMemcpyHostToDevice, st), "copy history offsets") ||
       !hip_ok(hipMemcpyAsync(ctx->d_u, &u, sizeof u, hipMemcpyHostToDevice, st), "copy u"))
     return -1;
+  vsmp_debug dbg{};
+  dbg.info = ctx->d_info;
   if (vsmp::pick_batch(ctx, ctx->d_logits, 1, n, ld, params, 0, H > 0 ? ctx->d_hist : nullptr,
                        H > 0 ? ctx->d_hoff : nullptr, VSMP_U_SUPPLIED, ctx->d_u, nullptr, 0, ctx->d_out,
-                       info ? ctx->d_info : nullptr, nullptr, nullptr, 0, st) != 0)
+                       info ? &dbg : nullptr, st) != 0)
     return -1;
   if (!hip_ok(hipMemcpyAsync(out_id, ctx->d_out, sizeof(int), hipMemcpyDeviceToHost, st), "copy id") ||
       (info && !hip_ok(hipMemcpyAsync(info, ctx->d_info, sizeof(vsmp_row_info), hipMemcpyDeviceToHost, st), "copy info")) ||
@@ -510,10 +553,11 @@ int vsmp_read_probe(vsmp_ctx* ctx, const void* p, long long bytes, void* stream)
   if (bytes <= 0 || bytes % 16 != 0 || reinterpret_cast<uintptr_t>(p) % 16 != 0)
     return vsmp::set_error("vsmp: read probe needs a positive multiple of 16 bytes at a 16-byte aligned address");
   if (!vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
-  if (!vsmp::grow(ctx->s_cnt, ctx->n_cnt, 8, false, "read probe sink")) return -1;
+  if (!vsmp::grow(ctx->s_cnt, ctx->n_cnt, 8, false, "read probe sink", ctx->done_ev)) return -1;
   hipStream_t st = static_cast<hipStream_t>(stream);  // NULL: the default stream, as for vsmp_pick_batch
   vsmp::launch_read_probe(p, bytes / 16, reinterpret_cast<unsigned*>(ctx->s_cnt), 16 * ctx->cus, st);
-  return vsmp::hip_ok(hipGetLastError(), "read-probe launch") ? 0 : -1;
+  if (!vsmp::hip_ok(hipGetLastError(), "read-probe launch")) return -1;
+  return vsmp::mark_done(ctx, st) ? 0 : -1;
 }
 
 int vsmp_exp_probe(vsmp_ctx* ctx, const double* x, double* y, long long n, void* stream) {

@@ -42,6 +42,7 @@ struct KArgs {
   int* cand_ids;
   double* cand_pr;
   int cand_cap;
+  uint32_t* pen_bits;  // diagnostics: [B][words] penalised-index bitmaps (zeroed by the call first)
   // slicing: row r is cut into S slices of L = kTpb * EPT elements
   int S;
   int L;
@@ -85,5 +86,6 @@ void launch_read_probe(const void* p, long long n16, unsigned* sink, int grid, h
 void launch_greedy_split(const KArgs& a, hipStream_t st);
 void launch_topk_split(const KArgs& a, hipStream_t st);
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st);
+void launch_zero_u32(uint32_t* p, long long n, hipStream_t st);
 
 }  // namespace vsmp

@@ -290,6 +290,31 @@ __device__ __forceinline__ bool map_block(int b, const KArgs& a, int& row, int& 
   return row < a.B;
 }
 
+// Diagnostics: words [w0, w0 + nw) of row `row`'s penalised-index bitmap, from the bitmap the
+// kernel penalises with (bits[0] is word w0), block-wide with NT threads.
+template <int NT>
+__device__ __forceinline__ void store_pen_words(const KArgs& a, int row, int w0, const uint32_t* bits, int nw) {
+  uint32_t* dst = a.pen_bits + static_cast<size_t>(row) * a.words + w0;
+  for (int i = threadIdx.x; i < nw; i += NT) dst[i] = bits[i];
+}
+
+// Diagnostics: the penalised ids of a part whose bitmap starts at element lo (bits[i] bit b is
+// element lo + 32 i + b; lo need not be a multiple of 32), OR-ed into the row's bitmap, which the
+// call zeroed first. Block-wide with NT threads.
+template <int NT>
+__device__ __forceinline__ void or_pen_ids(const KArgs& a, int row, int lo, const uint32_t* bits, int nw) {
+  uint32_t* dst = a.pen_bits + static_cast<size_t>(row) * a.words;
+  for (int i = threadIdx.x; i < nw; i += NT) {
+    uint32_t w = bits[i];
+    while (w) {
+      const int b = __ffs(static_cast<int>(w)) - 1;
+      w &= w - 1u;
+      const int id = lo + 32 * i + b;
+      atomicOr(&dst[id >> 5], 1u << (id & 31));
+    }
+  }
+}
+
 // Orders a wave's LDS writes before its later LDS reads of other lanes' entries.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -831,6 +856,7 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
       const int nw = (hi - lo + 31) >> 5;
       for (int i = tid; i < nw; i += kTpb) a.s_bits[static_cast<size_t>(row) * a.words + (lo >> 5) + i] = sm_bits[i];
     }
+    if (a.pen_bits) store_pen_words<kTpb>(a, row, lo >> 5, sm_bits, (hi - lo + 31) >> 5);  // lo: a multiple of 32
   } else {
     __syncthreads();
   }
@@ -1625,6 +1651,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       __syncthreads();
       g.R.bits = lb;
       g.R.lds_bits = true;
+      if (a.pen_bits) store_pen_words<kGenThreads>(a, row, 0, lb, a.words);
     }
     uint32_t mn = 0xFFFFFFFFu;
     gen_pass(g.R, [&](int e, float v) {
@@ -2037,6 +2064,35 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       a.info[row] = inf;
     }
   }
+  // Diagnostics: the first m = min(keep, cand_cap) elements of the draw set in sorted order (a
+  // prefix of the top-k prefix): the m-th composite by a count select, then every composite at or
+  // above it collected and sorted. A row marked for the exact redo gets its list from the redo.
+  if (a.cand_ids && a.cand_cap > 0 && !(a.x_flag && (flags & VSMP_FLAG_TOPP_NEAR))) {
+    const int m = min(keep, min(a.cand_cap, kGenCap));
+    const uint64_t ckk = g.ckk;
+    auto all_v = [](float) { return true; };
+    auto in_k = [ckk](uint64_t ck) { return ck >= ckk; };
+    __syncthreads();
+    const Sel s = refine_select<false>(g, sh, all_v, in_k, static_cast<uint64_t>(static_cast<uint32_t>(mnk)) << 32, mxc, k,
+                                       0, 0.0, static_cast<double>(m));
+    const uint64_t cm = s.ck;
+    if (tid == 0) sh.ints[4] = 0;
+    __syncthreads();
+    gen_pass(g.R, [&](int e, float v) {
+      const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
+      if (ck < cm || ck < ckk) return;
+      const int p = atomicAdd(&sh.ints[4], 1);
+      if (p < kGenCap) sh.list[p] = ck;
+    });
+    __syncthreads();
+    const int mm = min(sh.ints[4], m);
+    sort_desc(sh, sh.list, reinterpret_cast<uint64_t*>(sh.lpr), min(sh.ints[4], kGenCap));
+    for (int i = tid; i < mm; i += kGenThreads) {
+      const size_t o = static_cast<size_t>(row) * a.cand_cap + i;
+      a.cand_ids[o] = comp_idx(sh.list[i]);
+      if (a.cand_pr) a.cand_pr[o] = numer_g(g, comp_val(sh.list[i]));
+    }
+  }
 }
 
 // ---- exact redo of general rows whose top-p cut lies at rounding distance of top_p ------------
@@ -2052,6 +2108,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
 __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
   __shared__ int list[kGenThreads];
   __shared__ int nlist;
+  __shared__ int xkeep;
   const int tid = threadIdx.x;
   const int V = a.V, n2 = a.x_n;
   uint64_t* xs = reinterpret_cast<uint64_t*>(a.x_buf) + static_cast<size_t>(blockIdx.x) * 2 * static_cast<size_t>(n2);
@@ -2171,6 +2228,16 @@ __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
           inf.flags = (inf.flags & ~VSMP_FLAG_DRAW_NEAR) | VSMP_FLAG_SEQ_CUTS |
                       (inf.draw_margin < kNearDraw ? VSMP_FLAG_DRAW_NEAR : 0);
           a.info[row] = inf;
+        }
+        xkeep = keep;
+      }
+      __syncthreads();
+      if (a.cand_ids && a.cand_cap > 0) {  // diagnostics: the redone draw set replaces k_general's
+        const int m = min(xkeep, a.cand_cap);
+        for (int j = tid; j < m; j += kGenThreads) {
+          const size_t o = static_cast<size_t>(row) * a.cand_cap + j;
+          a.cand_ids[o] = comp_idx(xs[j]);
+          if (a.cand_pr) a.cand_pr[o] = pr[j];
         }
       }
       __syncthreads();  // the slot and the bitmap are reused by the next row
@@ -2586,6 +2653,7 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
     }
   }
   __syncthreads();
+  if (a.pen_bits && pen) store_pen_words<kRowNT>(a, row, 0, bits, words);
   const int k = path == kPathGreedy ? 1 : top_k_of(P, V);
   const int ks = min(k, V);
 
@@ -2910,6 +2978,7 @@ __global__ __launch_bounds__(kTkNT) void k_topk_split(KArgs a) {
     }
   }
   __syncthreads();
+  if (a.pen_bits && pen) or_pen_ids<kTkNT>(a, row, lo, sh.bits, words);
 
   // penalised order keys in place (0: past the part), the lane maximum and the part's maximum
   uint32_t lm = 0u;
@@ -3186,6 +3255,7 @@ __global__ __launch_bounds__(kSplitNT) void k_greedy_split(KArgs a) {
     for (int i = tid; i < words; i += kSplitNT) np += __popc(bits[i]);
     np = block_sum_u32<kSplitNT>(np, red32);
   }
+  if (a.pen_bits && pen) or_pen_ids<kSplitNT>(a, row, lo, bits, words);  // bits: complete (block_max64's barriers)
   if (tid == 0) {
     __hip_atomic_fetch_max(&a.g_slot[row], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (a.info) __hip_atomic_fetch_add(&a.g_npen[row], np, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -3226,6 +3296,12 @@ __global__ __launch_bounds__(256) void k_read_probe(const uint4* __restrict__ p,
   if (acc == 0x9E3779B9u) sink[blockIdx.x & 7] = acc;  // keeps the loads; the value is not used
 }
 
+// p[0, n) = 0 (the diagnostic bitmaps, before the kernels OR into them).
+__global__ __launch_bounds__(256) void k_zero_u32(uint32_t* __restrict__ p, long long n) {
+  const long long stride = static_cast<long long>(gridDim.x) * 256;
+  for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) p[i] = 0u;
+}
+
 // Diagnostics: y[i] = exp_tab(x[i]), the general path's exp, for measuring its accuracy.
 __global__ __launch_bounds__(256) void k_exp_probe(const double* __restrict__ x, double* __restrict__ y, long long n) {
   exp_tab_fill();
@@ -3239,6 +3315,11 @@ __global__ __launch_bounds__(256) void k_exp_probe(const double* __restrict__ x,
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st) {
   const long long blocks = std::min<long long>((n + 255) / 256, 4096);
   hipLaunchKernelGGL(k_exp_probe, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, x, y, n);
+}
+
+void launch_zero_u32(uint32_t* p, long long n, hipStream_t st) {
+  const long long blocks = std::max<long long>(1, std::min<long long>((n + 255) / 256, 2048));
+  hipLaunchKernelGGL(k_zero_u32, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, p, n);
 }
 
 void launch_topk_split(const KArgs& a, hipStream_t st) {
