@@ -131,6 +131,21 @@ VSMP_API int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, l
                              unsigned long long* rng_state, unsigned long long counter, int* out,
                              const vsmp_debug* dbg, void* stream);
 
+/* vsmp_pick_batch without any allocation and without a context. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture, serving loops
+ * that must not call hipMalloc, harnesses that forbid it). Same arguments, semantics and results
+ * as vsmp_pick_batch in row mode (VSMP_MODE=rows), with these limits: B <= 2048 rows, V <= 262144
+ * (2^18) logits; larger calls fail with an error. Its scratch (the exact redo's row marks, draws
+ * and sort slot) is one static device array of 4,218,880 bytes per GPU, held until the process
+ * ends and shared by every call on that GPU: calls that overlap on one GPU (on different streams,
+ * or from different threads) race and must not be issued. Per-row parameter batches run their
+ * general rows after the row kernel on `stream` (no second stream). Returns 0 or -1. */
+VSMP_API int vsmp_pick_batch_noalloc(const float* logits, int B, int V, long long ld,
+                                     const vsmp_params* params, int params_per_row, const int* hist,
+                                     const int* hist_off, int u_mode, const double* u,
+                                     unsigned long long* rng_state, unsigned long long counter,
+                                     int* out, const vsmp_debug* dbg, void* stream);
+
 /* One pick on a HOST logits row with a host history and a supplied draw u: the computation of
  * verbo::Sampler::pick(logits, n) (reference src/sampler.cpp:50-109) for a sampler whose history
  * is hist[0..H) and whose next stream draw is u. Copies the row to the device, runs the kernels

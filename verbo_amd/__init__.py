@@ -17,7 +17,7 @@ import numpy as np
 
 from .workloads import SAMPLING_DTYPE
 
-__all__ = ["Context", "Sampler", "Params", "RowInfo", "Debug", "VsmpError", "load_library", "U_SUPPLIED", "U_COUNTER",
+__all__ = ["Context", "Sampler", "Params", "RowInfo", "Debug", "VsmpError", "pick_batch_noalloc", "load_library", "U_SUPPLIED", "U_COUNTER",
            "U_XORSHIFT", "ROW_INFO_DTYPE", "SAMPLING_DTYPE"]
 __version__ = "0.1.0"
 
@@ -125,6 +125,9 @@ def load_library():
         "vsmp_pick_batch": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, _P, ctypes.c_int,
                                            _P, _P, ctypes.c_int, _P, _P, ctypes.c_ulonglong, _P,
                                            ctypes.POINTER(Debug), _P]),
+        "vsmp_pick_batch_noalloc": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, _P, ctypes.c_int,
+                                                   _P, _P, ctypes.c_int, _P, _P, ctypes.c_ulonglong, _P,
+                                                   ctypes.POINTER(Debug), _P]),
         "vsmp_pick_host": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.POINTER(Params), _P, ctypes.c_int,
                                           ctypes.c_double, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(RowInfo)]),
         "vsmp_sampler_new": (_P, [ctypes.POINTER(Params)]),
@@ -200,6 +203,55 @@ def pen_ids(bits, V):
     return [np.nonzero(r)[0].astype(np.int32) for r in flat]
 
 
+def _batch_args(logits, params, hist, hist_off, u_mode, u, rng_state, counter, out, info, cand_ids, cand_pr, pen_bits,
+                stream):
+    """The arguments of vsmp_pick_batch after the context, the output tensor, and the objects whose
+    addresses the arguments hold (kept alive by the caller until the call returns)."""
+    import torch
+
+    if logits.dim() != 2 or logits.dtype != torch.float32:
+        raise VsmpError("logits must be a 2-D float32 device tensor")
+    if not logits.is_cuda:
+        raise VsmpError("logits must be a device tensor")
+    B, V = logits.shape
+    ld = logits.stride(0)
+    if logits.stride(1) != 1:
+        raise VsmpError("logits rows must be contiguous")
+    if out is None:
+        out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    if isinstance(params, Params):
+        pp, per_row = ctypes.addressof(params), 0
+    else:
+        if params.numel() != 32 * B:
+            raise VsmpError("per-row params must hold B entries")
+        pp, per_row = _addr(params), 1
+    cap = cand_ids.shape[1] if cand_ids is not None else 0
+    if pen_bits is not None and pen_bits.numel() != B * ((V + 31) // 32):
+        raise VsmpError("pen_bits must hold B * ceil(V / 32) words")
+    dbg = None
+    if info is not None or cand_ids is not None or pen_bits is not None:
+        dbg = Debug(_addr(info), _addr(cand_ids), _addr(cand_pr), cap, _addr(pen_bits))
+    st = stream if stream is not None else torch.cuda.current_stream(logits.device)
+    args = (logits.data_ptr(), B, V, ld, pp, per_row, _addr(hist), _addr(hist_off), int(u_mode), _addr(u),
+            _addr(rng_state), int(counter), _addr(out), ctypes.byref(dbg) if dbg is not None else None,
+            ctypes.c_void_p(st.cuda_stream))
+    return args, out, (params, dbg)
+
+
+def pick_batch_noalloc(logits, params, hist=None, hist_off=None, u_mode=U_COUNTER, u=None, rng_state=None, counter=0,
+                       out=None, info=None, cand_ids=None, cand_pr=None, pen_bits=None, stream=None):
+    """vsmp_pick_batch_noalloc: Context.pick_batch's call without a context and without allocating
+    (row mode; B <= 2048, V <= 262144; the scratch is a static device array shared by every call on
+    the GPU, so calls must not overlap)."""
+    load_library()
+    args, out, keep = _batch_args(logits, params, hist, hist_off, u_mode, u, rng_state, counter, out, info, cand_ids,
+                                  cand_pr, pen_bits, stream)
+    if _lib.vsmp_pick_batch_noalloc(*args) != 0:
+        raise _err()
+    del keep
+    return out
+
+
 class Context:
     """A vsmp_ctx on one device: scratch for batched picks, staging for host picks."""
 
@@ -226,38 +278,11 @@ class Context:
         Diagnostics (vsmp_debug): info (uint8 [B*72]), cand_ids (int32 [B, cap]) / cand_pr (float64
         [B, cap]), pen_bits (int32 [B, ceil(V/32)]).
         Stream-ordered on `stream` (default: torch's current stream); does not synchronise."""
-        import torch
-
-        if logits.dim() != 2 or logits.dtype != torch.float32:
-            raise VsmpError("logits must be a 2-D float32 device tensor")
-        B, V = logits.shape
-        ld = logits.stride(0)
-        if logits.stride(1) != 1:
-            raise VsmpError("logits rows must be contiguous")
-        if out is None:
-            out = torch.empty(B, dtype=torch.int32, device=logits.device)
-        if isinstance(params, Params):
-            pp, per_row = ctypes.addressof(params), 0
-        else:
-            if params.numel() != 32 * B:
-                raise VsmpError("per-row params must hold B entries")
-            pp, per_row = _addr(params), 1
-        cap = 0
-        if cand_ids is not None:
-            cap = cand_ids.shape[1]
-        if pen_bits is not None and pen_bits.numel() != B * ((V + 31) // 32):
-            raise VsmpError("pen_bits must hold B * ceil(V / 32) words")
-        dbg = None
-        if info is not None or cand_ids is not None or pen_bits is not None:
-            dbg = Debug(_addr(info), _addr(cand_ids), _addr(cand_pr), cap, _addr(pen_bits))
-        st = stream if stream is not None else torch.cuda.current_stream(logits.device)
-        if not logits.is_cuda:
-            raise VsmpError("logits must be a device tensor")
-        rc = _lib.vsmp_pick_batch(self._h, logits.data_ptr(), B, V, ld, pp, per_row, _addr(hist), _addr(hist_off),
-                                  int(u_mode), _addr(u), _addr(rng_state), int(counter), _addr(out),
-                                  ctypes.byref(dbg) if dbg is not None else None, ctypes.c_void_p(st.cuda_stream))
-        if rc != 0:
+        args, out, keep = _batch_args(logits, params, hist, hist_off, u_mode, u, rng_state, counter, out, info,
+                                      cand_ids, cand_pr, pen_bits, stream)
+        if _lib.vsmp_pick_batch(self._h, *args) != 0:
             raise _err()
+        del keep
         return out
 
     def read_probe(self, t, stream=None):

@@ -278,16 +278,11 @@ Plan plan(const vsmp_ctx* ctx, int B, int V, const vsmp_params* hostp) {
   return pl;
 }
 
-int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
-                 int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
-                 unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
-                 hipStream_t st) {
-  vsmp_row_info* info = dbg ? dbg->info : nullptr;
-  int* cand_ids = dbg ? dbg->cand_ids : nullptr;
-  double* cand_pr = dbg ? dbg->cand_pr : nullptr;
+// Argument checks shared by the batched entry points (-1 with the message set, or 0).
+int check_batch(const float* logits, int B, int V, long long ld, const vsmp_params* params, const int* hist,
+                const int* hist_off, int u_mode, const double* u, unsigned long long* rng_state, int* out,
+                const vsmp_debug* dbg) {
   const int cand_cap = dbg ? dbg->cand_cap : 0;
-  uint32_t* pen_bits = dbg ? dbg->pen_bits : nullptr;
-  if (!ctx) return set_error("vsmp: null context");
   if (!logits || !out || !params) return set_error("vsmp: logits, params and out are required");
   if (B < 1 || V < 1) return set_error("vsmp: need B >= 1 and V >= 1");
   if (V > kMaxVocab) return set_error("vsmp: vocabulary larger than " + std::to_string(kMaxVocab));
@@ -297,38 +292,15 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
   if (u_mode == VSMP_U_SUPPLIED && !u) return set_error("vsmp: u is required with VSMP_U_SUPPLIED");
   if (u_mode == VSMP_U_XORSHIFT && !rng_state) return set_error("vsmp: rng_state is required with VSMP_U_XORSHIFT");
   if (u_mode < VSMP_U_SUPPLIED || u_mode > VSMP_U_XORSHIFT) return set_error("vsmp: unknown u_mode");
-  if (cand_cap < 0 || (cand_cap > 0 && !cand_ids)) return set_error("vsmp: cand_ids is required with cand_cap > 0");
+  if (cand_cap < 0 || (cand_cap > 0 && !dbg->cand_ids)) return set_error("vsmp: cand_ids is required with cand_cap > 0");
   if (cand_cap > kGenCap) return set_error("vsmp: cand_cap is at most " + std::to_string(kGenCap));
-  const Plan pl = plan(ctx, B, V, params_per_row ? nullptr : params);
-  const size_t slots = static_cast<size_t>(B) * static_cast<size_t>(pl.S);
-  if (slots > static_cast<size_t>(INT32_MAX) / kKmax) return set_error("vsmp: batch too large");
-  const int words = (V + 31) / 32;
-  hipEvent_t busy = ctx->done_ev;
-  if (!grow(ctx->s_cnt, ctx->n_cnt, slots, false, "scratch", busy) ||
-      !grow(ctx->s_npen, ctx->n_npen, slots, false, "scratch", busy) ||
-      !grow(ctx->s_max, ctx->n_max, slots, false, "scratch", busy) ||
-      !grow(ctx->s_min, ctx->n_min, slots, false, "scratch", busy))
-    return -1;
-  if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch", busy)) return -1;
-  // General rows marked near a top-p tie are redone exactly (rows up to kExactMaxVocab). The scratch
-  // is sized whenever a batch may hold general rows, whatever its parameters, so that one call at a
-  // shape sizes it for every later call at that shape (graph capture); the launch is skipped for
-  // shared parameters without a top-p cut, which mark no row.
-  const bool exact_scratch = pl.any_general && V <= kExactMaxVocab;
-  const bool exact = exact_scratch && (params_per_row || (params->top_p > 0.0f && params->top_p < 1.0f));
-  int x_n = 1;
-  while (x_n < V) x_n <<= 1;
-  if (exact_scratch && (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch", busy) ||
-                        !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch", busy) ||
-                        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(kExactSlots) * 2 * x_n, false, "scratch", busy)))
-    return -1;
-  if (pl.any_general && !pl.rows && !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch", busy))
-    return -1;
-  if (pen_bits) {  // diagnostics: the kernels store or OR each row's penalised ids into zeroed bitmaps
-    launch_zero_u32(pen_bits, static_cast<long long>(B) * words, st);
-    if (!hip_ok(hipGetLastError(), "zero-fill launch")) return -1;
-  }
+  return 0;
+}
 
+// The kernels' arguments that do not depend on the plan or the scratch.
+KArgs batch_args(const float* logits, int B, int V, long long ld, const vsmp_params* params, int params_per_row,
+                 const int* hist, const int* hist_off, int u_mode, const double* u, unsigned long long* rng_state,
+                 unsigned long long counter, int* out, const vsmp_debug* dbg) {
   KArgs a{};
   a.logits = logits;
   a.ld = ld;
@@ -347,11 +319,53 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
   a.rng = rng_state;
   a.counter = counter;
   a.out = out;
-  a.info = info;
-  a.cand_ids = cand_ids;
-  a.cand_pr = cand_pr;
-  a.cand_cap = cand_cap;
-  a.pen_bits = pen_bits;
+  if (dbg) {
+    a.info = dbg->info;
+    a.cand_ids = dbg->cand_ids;
+    a.cand_pr = dbg->cand_pr;
+    a.cand_cap = dbg->cand_cap;
+    a.pen_bits = dbg->pen_bits;
+  }
+  a.words = (V + 31) / 32;
+  int x_n = 1;
+  while (x_n < V) x_n <<= 1;
+  a.x_n = x_n;
+  return a;
+}
+
+int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
+                 int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
+                 unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
+                 hipStream_t st) {
+  if (check_batch(logits, B, V, ld, params, hist, hist_off, u_mode, u, rng_state, out, dbg) != 0) return -1;
+  KArgs a = batch_args(logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter, out, dbg);
+  const Plan pl = plan(ctx, B, V, params_per_row ? nullptr : params);
+  const size_t slots = static_cast<size_t>(B) * static_cast<size_t>(pl.S);
+  if (slots > static_cast<size_t>(INT32_MAX) / kKmax) return set_error("vsmp: batch too large");
+  const int words = a.words;
+  hipEvent_t busy = ctx->done_ev;
+  if (!grow(ctx->s_cnt, ctx->n_cnt, slots, false, "scratch", busy) ||
+      !grow(ctx->s_npen, ctx->n_npen, slots, false, "scratch", busy) ||
+      !grow(ctx->s_max, ctx->n_max, slots, false, "scratch", busy) ||
+      !grow(ctx->s_min, ctx->n_min, slots, false, "scratch", busy))
+    return -1;
+  if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch", busy)) return -1;
+  // General rows marked near a top-p tie are redone exactly (rows up to kExactMaxVocab). The scratch
+  // is sized whenever a batch may hold general rows, whatever its parameters, so that one call at a
+  // shape sizes it for every later call at that shape (graph capture); the launch is skipped for
+  // shared parameters without a top-p cut, which mark no row.
+  const bool exact_scratch = pl.any_general && V <= kExactMaxVocab;
+  const bool exact = exact_scratch && (params_per_row || (params->top_p > 0.0f && params->top_p < 1.0f));
+  if (exact_scratch && (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch", busy) ||
+                        !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch", busy) ||
+                        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(kExactSlots) * 2 * a.x_n, false, "scratch", busy)))
+    return -1;
+  if (pl.any_general && !pl.rows && !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch", busy))
+    return -1;
+  if (a.pen_bits) {  // diagnostics: the kernels store or OR each row's penalised ids into zeroed bitmaps
+    launch_zero_u32(a.pen_bits, static_cast<long long>(B) * words, st);
+    if (!hip_ok(hipGetLastError(), "zero-fill launch")) return -1;
+  }
   a.S = pl.S;
   a.L = pl.L;
   a.xcd_map = pl.xcd;
@@ -362,12 +376,10 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
   a.s_max = ctx->s_max;
   a.s_min = ctx->s_min;
   a.s_bits = ctx->s_bits;
-  a.words = words;
   a.gen_fused = pl.rows ? 1 : 0;
   a.x_flag = exact ? ctx->x_flag : nullptr;
   a.x_u = ctx->x_u;
   a.x_buf = ctx->x_buf;
-  a.x_n = x_n;
   if (pl.split) {
     if (!grow(ctx->g_slot, ctx->n_slot, static_cast<size_t>(B), true, "scratch", busy, st) ||
         !grow(ctx->g_tick, ctx->n_tick, static_cast<size_t>(B), true, "scratch", busy, st) ||
@@ -390,7 +402,7 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
     launch_general(a, ctx->side);
     bool ok = hip_ok(hipGetLastError(), "general-path launch");
     if (ok && exact) {
-      launch_general_exact(a, ctx->side);
+      launch_general_exact(a, kExactSlots, ctx->side);
       ok = hip_ok(hipGetLastError(), "exact general-path launch");
     }
     if (!hip_ok(hipEventRecord(ctx->join_ev, ctx->side), "hipEventRecord")) return -1;
@@ -419,7 +431,7 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
     launch_general(a, st);
     if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
     if (exact) {
-      launch_general_exact(a, st);
+      launch_general_exact(a, kExactSlots, st);
       if (!hip_ok(hipGetLastError(), "exact general-path launch")) return -1;
     }
   }
@@ -444,6 +456,55 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
                               out, dbg, st);
   if (!mark_done(ctx, st)) return -1;
   return rc;
+}
+
+// vsmp_pick_batch_noalloc: row mode, one stream, the scratch in the static device array.
+int pick_batch_noalloc(const float* logits, int B, int V, long long ld, const vsmp_params* params, int params_per_row,
+                       const int* hist, const int* hist_off, int u_mode, const double* u,
+                       unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
+                       hipStream_t st) {
+  if (check_batch(logits, B, V, ld, params, hist, hist_off, u_mode, u, rng_state, out, dbg) != 0) return -1;
+  if (B > kNoAllocMaxRows || V > kNoAllocMaxVocab)
+    return set_error("vsmp: vsmp_pick_batch_noalloc takes at most " + std::to_string(kNoAllocMaxRows) + " rows of at most " +
+                     std::to_string(kNoAllocMaxVocab) + " logits (got " + std::to_string(B) + " x " + std::to_string(V) + ")");
+  unsigned char* scr = nullptr;
+  if (!hip_ok(static_scratch(&scr), "address of the static scratch")) return -1;
+  KArgs a = batch_args(logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter, out, dbg);
+  a.S = 1;
+  a.L = V;
+  a.xcd_map = 0;
+  a.smallk_ok = 1;
+  a.gen_fused = 1;  // k_general takes its rows' maximum, minimum and penalty bitmap itself, in LDS
+  // every general row's mark and draw are written by k_general before k_general_exact reads them,
+  // so nothing of the array needs clearing between calls
+  a.x_flag = reinterpret_cast<int*>(scr + kNoAllocFlagOff);
+  a.x_u = reinterpret_cast<double*>(scr + kNoAllocUOff);
+  a.x_buf = reinterpret_cast<unsigned long long*>(scr + kNoAllocBufOff);
+  bool any_general = true, any_rows = true, exact = true;
+  if (!params_per_row) {
+    const int path = path_host(*params, V, true);
+    any_general = path == kPathGeneral;
+    any_rows = !any_general;
+    exact = any_general && params->top_p > 0.0f && params->top_p < 1.0f;
+  }
+  if (!exact) a.x_flag = nullptr;
+  if (a.pen_bits) {
+    launch_zero_u32(a.pen_bits, static_cast<long long>(B) * a.words, st);
+    if (!hip_ok(hipGetLastError(), "zero-fill launch")) return -1;
+  }
+  if (any_rows) {  // k_rows leaves general rows alone (gen_fused)
+    launch_rows(a, st);
+    if (!hip_ok(hipGetLastError(), "row launch")) return -1;
+  }
+  if (any_general) {
+    launch_general(a, st);
+    if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
+    if (exact) {
+      launch_general_exact(a, 1, st);  // one sort slot: marked rows are redone one after another
+      if (!hip_ok(hipGetLastError(), "exact general-path launch")) return -1;
+    }
+  }
+  return 0;
 }
 
 }  // namespace
@@ -505,6 +566,15 @@ int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long 
   if (ctx && !vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
   return vsmp::pick_batch(ctx, logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
                           out, dbg, static_cast<hipStream_t>(stream));
+}
+
+int vsmp_pick_batch_noalloc(const float* logits, int B, int V, long long ld, const vsmp_params* params,
+                            int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
+                            unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
+                            void* stream) {
+  vsmp::clear_error();
+  return vsmp::pick_batch_noalloc(logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
+                                  out, dbg, static_cast<hipStream_t>(stream));
 }
 
 int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params* params, const int* hist, int H,

@@ -79,9 +79,21 @@ void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st);
 void launch_finish(const KArgs& a, hipStream_t st);
 void launch_rows(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
-void launch_general_exact(const KArgs& a, hipStream_t st);
+void launch_general_exact(const KArgs& a, int slots, hipStream_t st);
 constexpr int kExactSlots = 8;            // workgroups (and scratch slots) of k_general_exact
 constexpr int kExactMaxVocab = 1 << 20;   // k_general_exact's reach (larger rows keep the flag)
+
+// vsmp_pick_batch_noalloc: row mode only, within these limits, on one static device array per GPU
+// holding the exact redo's marks and draws (kNoAllocMaxRows each) and one sort slot (2 x 2^18
+// composites): 4,218,880 bytes.
+constexpr int kNoAllocMaxRows = 2048;
+constexpr int kNoAllocMaxVocab = 1 << 18;
+constexpr size_t kNoAllocFlagOff = 0;
+constexpr size_t kNoAllocUOff = kNoAllocFlagOff + sizeof(int) * kNoAllocMaxRows;
+constexpr size_t kNoAllocBufOff = kNoAllocUOff + sizeof(double) * kNoAllocMaxRows;
+constexpr size_t kNoAllocScratchBytes = kNoAllocBufOff + 2 * sizeof(uint64_t) * static_cast<size_t>(kNoAllocMaxVocab);
+// The calling thread's current device's address of that array, taken once per device.
+hipError_t static_scratch(unsigned char** out);
 void launch_read_probe(const void* p, long long n16, unsigned* sink, int grid, hipStream_t st);
 void launch_greedy_split(const KArgs& a, hipStream_t st);
 void launch_topk_split(const KArgs& a, hipStream_t st);

@@ -30,6 +30,7 @@
 //  k_exp_probe   the general path's fp64 exp over an array, for measuring its accuracy.
 #include <algorithm>
 #include <cfloat>
+#include <mutex>
 #include <type_traits>
 
 #include "vsmp_common.hpp"
@@ -3363,7 +3364,7 @@ void launch_rows(const KArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(k_rows, dim3(a.B), dim3(kRowNT), dyn, st, a);
 }
 
-void launch_general_exact(const KArgs& a, hipStream_t st) {
+void launch_general_exact(const KArgs& a, int slots, hipStream_t st) {
   const size_t bytes = static_cast<size_t>(a.words) * sizeof(uint32_t);
   const size_t dyn = (a.hist_off != nullptr && a.gen_fused && bytes <= kGenBitsLds) ? bytes : 0;
   static bool configured = false;
@@ -3372,7 +3373,7 @@ void launch_general_exact(const KArgs& a, hipStream_t st) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGenBitsLds));
     configured = true;
   }
-  hipLaunchKernelGGL(k_general_exact, dim3(std::min(a.B, kExactSlots)), dim3(kGenThreads), dyn, st, a);
+  hipLaunchKernelGGL(k_general_exact, dim3(std::min(a.B, slots)), dim3(kGenThreads), dyn, st, a);
 }
 
 void launch_general(const KArgs& a, hipStream_t st) {
@@ -3385,6 +3386,33 @@ void launch_general(const KArgs& a, hipStream_t st) {
     configured = true;
   }
   hipLaunchKernelGGL(k_general, dim3(a.B), dim3(kGenThreads), dyn, st, a);
+}
+
+// ---- the scratch of vsmp_pick_batch_noalloc ---------------------------------------------------
+//
+// One array per GPU, loaded with the code object and held until the process ends. In host code its
+// name stands for the symbol only: the device address comes from hipGetSymbolAddress, taken once
+// per device with that device current, and is what the launches receive.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+hipError_t static_scratch(unsigned char** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static unsigned char* addr[kMaxDevices] = {};
+  *out = nullptr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    addr[dev] = static_cast<unsigned char*>(p);
+  }
+  *out = addr[dev];
+  return hipSuccess;
 }
 
 }  // namespace vsmp
