@@ -86,6 +86,107 @@ def cpu_baseline(w, budget):
     return out
 
 
+def bench_single(args):
+    """The single-row decode workload as the survey states it: 10,000 consecutive draws on one fixed
+    1 x 49152 row and history (seed 42, no accept between draws). Reports microseconds per draw for
+    the device-resident calls (value: draws/s), the same calls replayed from a HIP graph (100 per
+    graph), the drop-in verbo::Sampler::pick on a host row (the path verbo's generate takes: the row
+    copied to the device, the id copied back, one synchronisation per pick, plus the ctypes call from
+    Python), and the reference's pick on the host CPU (oracle/_ref) on the same row."""
+    import numpy as np
+    import torch
+
+    import verbo_amd as V
+    from verbo_amd import workloads as W
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    w = W.make("single")
+    p0 = w.params[0]
+    prm = V.Params(*[p0[f].item() for f in V.SAMPLING_DTYPE.names])
+    dev = torch.device("cuda:0")
+    d = torch.from_numpy(w.logits).to(dev)
+    h, ho = torch.from_numpy(w.hist).to(dev), torch.from_numpy(w.hist_off).to(dev)
+    st0 = O.rng_seed(int(p0["seed"]))
+    rng = torch.from_numpy(np.array([st0[0], st0[1]], np.uint64).view(np.int64)).to(dev)
+    n = args.draws
+    out = torch.empty(n, dtype=torch.int32, device=dev)
+    ctx = V.Context(0)
+    stream = torch.cuda.current_stream(dev)
+
+    def eager(k):
+        for i in range(k):
+            ctx.pick_batch(d, prm, h, ho, V.U_XORSHIFT, rng_state=rng, out=out[i:i + 1], stream=stream)
+
+    eager(args.warmup)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    eager(n)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us_eager = e0.elapsed_time(e1) * 1e3 / n
+    log(f"[bench] single: {n} device-resident calls, {us_eager:.2f} us per draw")
+    per = 100
+    g = torch.cuda.CUDAGraph()
+    gs = torch.cuda.Stream()
+    with torch.cuda.stream(gs):
+        with torch.cuda.graph(g, stream=gs):
+            for i in range(per):
+                ctx.pick_batch(d, prm, h, ho, V.U_XORSHIFT, rng_state=rng, out=out[i:i + 1], stream=gs)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(n // per):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us_graph = e0.elapsed_time(e1) * 1e3 / (n // per * per)
+    log(f"[bench] single: graph replays, {us_graph:.2f} us per draw")
+    s = V.Sampler(prm)
+    for t in w.hist:
+        s.accept(int(t))
+    row = np.ascontiguousarray(w.logits[0])
+    for _ in range(args.warmup):
+        s.pick(row)
+    k = min(n, 2000)
+    t0 = time.perf_counter()
+    for _ in range(k):
+        s.pick(row)
+    us_host = (time.perf_counter() - t0) * 1e6 / k
+    log(f"[bench] single: drop-in Sampler::pick on a host row, {us_host:.2f} us per draw")
+    cpu = None
+    if args.cpu_budget > 0 and O.ref_available():
+        c = O.Sampling(*[p0[f].item() for f in O.SAMPLING_DTYPE.names])
+        m = 2000
+        t0 = time.perf_counter()
+        O.ref_sampler_run(w.logits[0], c, w.hist, n_picks=m)
+        secs = time.perf_counter() - t0
+        cpu = {"value": m / secs, "unit": "draws/s", "cores": 1, "kind": "reference",
+               "sample": f"{m} consecutive pick() calls of one reference Sampler on the same row, 1 thread"}
+    return {
+        "metric": "single-row draws/s, " + DESCR["single"] + ", 10,000 consecutive draws",
+        "value": 1e6 / us_eager,
+        "unit": "draws/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": args.warmup,
+        "ms_per_step": us_eager * 1e-3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": DESCR["single"], "B": 1, "V": w.V, "draw_stream": "the reference's xorshift128+ "
+                   "on the device (VSMP_U_XORSHIFT)", "epilogue_dtype": "f64"},
+        "us_per_draw": {"device_resident": us_eager, "graph_replay": us_graph, "drop_in_host_row": us_host},
+        "roofline": None,
+        "cpu_baseline": cpu,
+    }
+
+
 def traffic_from_profiles(name):
     """HBM bytes per call measured by rocprofv3 PMC runs (profiles/<workload>_traffic.json)."""
     p = ROOT / "profiles" / f"{name}_traffic.json"
@@ -105,6 +206,7 @@ def main():
     ap.add_argument("--workload", default="peaked", choices=sorted(DESCR))
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0: skip)")
     ap.add_argument("--min-buffer-mb", type=float, default=640.0)
+    ap.add_argument("--draws", type=int, default=10000, help="single workload: consecutive draws timed")
     ap.add_argument("--copy", action="store_true",
                     help="time a plain device copy of one logits buffer per step instead (the known-size kernel "
                          "that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -121,6 +223,9 @@ def main():
     from verbo_amd import workloads as W
 
     assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    if args.workload == "single":
+        print(json.dumps(bench_single(args)), flush=True)
+        return
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()
     w = W.make(args.workload)

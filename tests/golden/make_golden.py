@@ -28,6 +28,7 @@ import oracle as O  # noqa: E402
 from verbo_amd import workloads as W  # noqa: E402
 
 OUT = Path(__file__).resolve().parent / "sampler_golden.npz"
+SINGLE = Path(__file__).resolve().parent / "single_draws_golden.npz"
 
 
 def cfg_arr(c):
@@ -118,5 +119,19 @@ def main():
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(cases)} cases, {wl} workload rows)")
 
 
+def single_draws(n=10000):
+    """The single-row workload's 10,000 consecutive draws (1 x 49152, seed 42, its 64-id history
+    accepted first, no accept between draws) from the compiled reference Sampler: ids[n], the
+    row's sha256 (the logits are regenerated from verbo_amd.workloads) and its parameters."""
+    w = W.make("single")
+    p = w.params[0].copy()
+    c = O.Sampling(*[p[f].item() for f in O.SAMPLING_DTYPE.names])
+    ids = O.ref_sampler_run(w.logits[0], c, w.hist, n_picks=n, accept_each=False)
+    np.savez_compressed(SINGLE, ids=ids.astype(np.int32), cfg=cfg_arr(c),
+                        sha=np.frombuffer(hashlib.sha256(w.logits[0].tobytes()).digest(), np.uint8))
+    print(f"wrote {SINGLE} ({n} draws, {len(np.unique(ids))} distinct ids)")
+
+
 if __name__ == "__main__":
     main()
+    single_draws()

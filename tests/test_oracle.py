@@ -207,3 +207,20 @@ def test_minp_topp_cuts_closed_form(oracle):
         want = min(keep, int(hit[0]) + 1) if hit.size else keep
         if info.topp_margin > 1e-12:
             assert info.keep == want, (t, info.keep, want)
+
+
+def test_single_workload_10000_draws(oracle):
+    """The oracle's Sampler run reproduces the compiled reference's 10,000 consecutive draws on the
+    single-row workload (tests/golden/single_draws_golden.npz: seed 42, history accepted, no accept
+    between draws)."""
+    from pathlib import Path
+
+    from verbo_amd import workloads as W
+
+    z = np.load(Path(__file__).resolve().parent / "golden" / "single_draws_golden.npz", allow_pickle=False)
+    w = W.make("single")
+    assert hashlib.sha256(w.logits[0].tobytes()).digest() == bytes(z["sha"])
+    c = z["cfg"][0]
+    cfg = oracle.Sampling(*[c[f].item() for f in oracle.SAMPLING_DTYPE.names])
+    ids = oracle.sampler_run(w.logits[0], cfg, w.hist, n_picks=int(z["ids"].size))
+    assert (ids == z["ids"]).all()
