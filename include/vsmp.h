@@ -178,6 +178,51 @@ VSMP_API void vsmp_sampler_accept(vsmp_sampler* s, int tok);
 /* Sampler::reset, src/sampler.cpp:26-31. */
 VSMP_API void vsmp_sampler_reset(vsmp_sampler* s);
 
+/* ---- device-resident decode state ----------------------------------------------------------
+ * The reference decodes from a host row: Session::eval returns the logits on the host
+ * (src/session.cpp:196-200) and generate picks from it (src/sampler.cpp:157-173). When an LM head
+ * leaves its logits on the GPU, these objects keep everything else there too: the draw stream
+ * (verbo::Sampler's xorshift128+, seeded as Sampler::reset seeds it, src/sampler.cpp:24-41) and
+ * the history window (Sampler::accept's trimming, :43-48) live in device memory and are updated by
+ * the kernels, so that per token only the picked id crosses to the host. */
+
+/* One sequence: verbo::Sampler with its state on device `device` (a context of its own). */
+typedef struct vsmp_dsampler vsmp_dsampler;
+/* Sampler::Sampler(Sampling), src/sampler.cpp:24. NULL on error. */
+VSMP_API vsmp_dsampler* vsmp_dsampler_new(int device, const vsmp_params* cfg);
+VSMP_API void vsmp_dsampler_free(vsmp_dsampler* s);
+/* Sampler::reset, src/sampler.cpp:26-31 (reseeds; clears the history). Returns 0 or -1. */
+VSMP_API int vsmp_dsampler_reset(vsmp_dsampler* s);
+/* Sampler::accept for ids[0..n) in order (host array, e.g. a prompt), stream-ordered on
+ * `stream`. Returns 0 or -1. */
+VSMP_API int vsmp_dsampler_accept(vsmp_dsampler* s, const int* ids, int n, void* stream);
+/* Sampler::pick on device logits (n floats, 16-byte aligned, readable up to the next multiple
+ * of 4 floats), on `stream`: the pick's draw comes from the device stream, which advances as
+ * Sampler::unit would. vsmp_dsampler_pick returns the id (it copies 4 bytes back and waits);
+ * vsmp_dsampler_pick_async writes it to device `out` and does not wait. -1 on error. */
+VSMP_API int vsmp_dsampler_pick(vsmp_dsampler* s, const float* logits, int n, void* stream);
+VSMP_API int vsmp_dsampler_pick_async(vsmp_dsampler* s, const float* logits, int n, int* out, void* stream);
+
+/* A batch of sequences decoded together (a continuous-batching server step; the reference serves
+ * one request at a time, cli/serve.cpp:168): n independent verbo::Samplers with per-row
+ * parameters (params: HOST array of n), each history window in a device region of `cap` ids
+ * (cap >= 4 * repeat_last for every row with repeat_last > 0; for the others, the most ids a
+ * sequence may accept). NULL on error. */
+typedef struct vsmp_bsampler vsmp_bsampler;
+VSMP_API vsmp_bsampler* vsmp_bsampler_new(int device, int n, const vsmp_params* params, int cap);
+VSMP_API void vsmp_bsampler_free(vsmp_bsampler* s);
+/* Sampler::accept of ids[0..m) (host array, e.g. a prompt) for row `row`; synchronous. 0 or -1. */
+VSMP_API int vsmp_bsampler_accept_host(vsmp_bsampler* s, int row, const int* ids, int m);
+/* One pick per row from device logits [n][ld] (V logits per row), ids to device out[n], on
+ * `stream`; each row's draw comes from its own device stream. 0 or -1. */
+VSMP_API int vsmp_bsampler_pick(vsmp_bsampler* s, const float* logits, int V, long long ld, int* out, void* stream);
+/* Sampler::accept of device ids[r] for every row r with active[r] != 0 (device arrays; active
+ * NULL: every row), on `stream`: the histories grow on the device. 0 or -1. */
+VSMP_API int vsmp_bsampler_accept(vsmp_bsampler* s, const int* ids, const int* active, void* stream);
+/* 1 if an accept found a row's region full (repeat_last <= 0 and cap ids accepted; that id was
+ * dropped), else 0; waits for `stream`. -1 on error. */
+VSMP_API int vsmp_bsampler_full(vsmp_bsampler* s, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -126,6 +126,12 @@ def load_ref():
         lib.vref_pick_rows.restype = ctypes.c_int
         lib.vref_pick_rows.argtypes = [_P, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, _P, ctypes.c_int, _P, _P,
                                        _P, ctypes.c_int]
+        lib.vref_sampler_new.restype = ctypes.c_void_p
+        lib.vref_sampler_new.argtypes = [ctypes.POINTER(Sampling)]
+        lib.vref_sampler_free.argtypes = [ctypes.c_void_p]
+        lib.vref_sampler_accept.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        lib.vref_sampler_pick.restype = ctypes.c_int
+        lib.vref_sampler_pick.argtypes = [ctypes.c_void_p, _P, ctypes.c_int]
         lib.vref_time_rows.restype = ctypes.c_double
         lib.vref_time_rows.argtypes = [_P, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, _P, ctypes.c_int, _P, _P,
                                        ctypes.c_int, ctypes.c_double, ctypes.POINTER(ctypes.c_longlong)]
@@ -266,3 +272,23 @@ def ref_time_rows(logits, params, hist=None, hist_off=None, threads=1, budget_s=
     s = lib.vref_time_rows(_ptr(lg), B, V, V, _ptr(params), per_row, _ptr(h), _ptr(ho), threads, budget_s,
                            ctypes.byref(n))
     return s, n.value
+
+
+class RefSampler:
+    """A reference verbo::Sampler (compiled from its sources) behind a handle: pick / accept."""
+
+    def __init__(self, cfg):
+        self._lib = load_ref()
+        self._h = self._lib.vref_sampler_new(ctypes.byref(cfg))
+
+    def pick(self, logits):
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        return self._lib.vref_sampler_pick(self._h, _ptr(lg), lg.size)
+
+    def accept(self, tok):
+        self._lib.vref_sampler_accept(self._h, int(tok))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            self._lib.vref_sampler_free(self._h)
+            self._h = None

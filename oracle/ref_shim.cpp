@@ -110,3 +110,12 @@ VREF_API double vref_time_rows(const float* logits, int B, int V, long long ld, 
   *picks = done.load();
   return s;
 }
+
+// One reference verbo::Sampler behind a handle, for recorders that interleave picks and accepts
+// across several samplers (the batched decode golden).
+VREF_API void* vref_sampler_new(const verbo::Sampling* cfg) { return new verbo::Sampler(*cfg); }
+VREF_API void vref_sampler_free(void* s) { delete static_cast<verbo::Sampler*>(s); }
+VREF_API void vref_sampler_accept(void* s, int tok) { static_cast<verbo::Sampler*>(s)->accept(tok); }
+VREF_API int vref_sampler_pick(void* s, const float* logits, int n) {
+  return static_cast<verbo::Sampler*>(s)->pick(logits, n);
+}

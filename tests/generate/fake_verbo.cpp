@@ -2,10 +2,11 @@
 // interface (reference include/verbo/verbo.hpp), and a driver that runs a fixed list of decode
 // scenarios through verbo::generate and prints one JSON line per scenario.
 //
-// TEST INFRASTRUCTURE. Built twice from this one file: against the reference's header and its
-// src/sampler.cpp (oracle/Makefile, target _ref/gen_ref: the golden outputs) and against this
+// TEST INFRASTRUCTURE. Built three times from this one file: against the reference's header and its
+// src/sampler.cpp (oracle/Makefile, target _ref/gen_ref: the golden outputs), against this
 // repository's header and libvsmp.so (tests/generate/Makefile, gen_ours: the GPU sampler under
-// the drop-in generate). The scenarios exercise the loop's ordering (src/sampler.cpp:111-181):
+// the drop-in generate), and with VSMP_DEVICE_GENERATE (gen_ours_device: the device-resident
+// generate_device, its logits copied to the device as an LM head on the GPU would leave them). The scenarios exercise the loop's ordering (src/sampler.cpp:111-181):
 // stop ids, stop strings split across tokens (the hold-back), a callback that stops, the context
 // limit, max_tokens, the detokeniser's held text and its flush, greedy and sampled picks.
 #include <cmath>
@@ -15,6 +16,11 @@
 #include <vector>
 
 #include "verbo/verbo.hpp"
+#ifdef VSMP_DEVICE_GENERATE
+#include <hip/hip_runtime.h>
+
+#include "vsmp_generate.hpp"
+#endif
 
 namespace {
 
@@ -129,6 +135,39 @@ std::string Detok::flush() {
 
 namespace {
 
+#ifdef VSMP_DEVICE_GENERATE
+// The test double's session as a device-resident LM head would present it (the device generate
+// variant, gen_ours_device): each evaluation's logits are written to a device buffer on the
+// session's stream, as an LM head's output would be.
+class DeviceFake : public vsmp::DeviceSession {
+ public:
+  explicit DeviceFake(verbo::Session& s) : s_(s) {
+    (void)hipStreamCreateWithFlags(&st_, hipStreamNonBlocking);
+    (void)hipMalloc(reinterpret_cast<void**>(&d_), sizeof(float) * static_cast<size_t>((g_sc->vocab + 3) & ~3));
+  }
+  ~DeviceFake() override {
+    (void)hipStreamSynchronize(st_);
+    (void)hipFree(d_);
+    (void)hipStreamDestroy(st_);
+  }
+  const float* eval(const int* ids, int n) override {
+    const float* h = s_.eval(ids, n);
+    // the host row stays unchanged until the next eval, which follows the pick's wait for this stream
+    (void)hipMemcpyAsync(d_, h, sizeof(float) * static_cast<size_t>(g_sc->vocab), hipMemcpyHostToDevice, st_);
+    return d_;
+  }
+  int pos() const override { return s_.pos(); }
+  int ctx() const override { return s_.ctx(); }
+  const verbo::Model& model() const override { return s_.model(); }
+  void* stream() const override { return st_; }
+
+ private:
+  verbo::Session& s_;
+  hipStream_t st_ = nullptr;
+  float* d_ = nullptr;
+};
+#endif
+
 std::string json_str(const std::string& s) {
   std::string o = "\"";
   for (const char c : s) {
@@ -176,11 +215,17 @@ int main() {
     o.stop_text = sc.stop_text;
     std::vector<std::string> chunks;
     int calls = 0;
-    const verbo::Stats st = verbo::generate(ses, sc.prompt, o, [&](std::string_view t) {
+    const auto on_text = [&](std::string_view t) {
       chunks.emplace_back(t);
       ++calls;
       return !(sc.cb_limit > 0 && calls >= sc.cb_limit);
-    });
+    };
+#ifdef VSMP_DEVICE_GENERATE
+    DeviceFake dev(ses);
+    const verbo::Stats st = vsmp::generate_device(dev, sc.prompt, o, on_text);
+#else
+    const verbo::Stats st = verbo::generate(ses, sc.prompt, o, on_text);
+#endif
     std::string line = std::string("{\"name\": ") + json_str(sc.name) + ", \"prompt\": " + std::to_string(st.prompt) +
                        ", \"gen\": " + std::to_string(st.gen) + ", \"stopped\": " + (st.stopped ? "true" : "false") +
                        ", \"pos\": " + std::to_string(ses.pos()) + ", \"toks\": [";

@@ -6,7 +6,10 @@ strings split across tokens (hold-back), a callback that stops, the context limi
 text held by the detokeniser and flushed, greedy and sampled picks with penalties.
 - golden: the reference's own generate + Sampler, compiled from its sources (oracle/_ref/gen_ref),
   recorded in tests/golden/generate_golden.jsonl;
-- ours: verbo_amd/csrc/generate.cpp + the GPU Sampler of libvsmp.so (tests/generate/gen_ours).
+- ours: verbo_amd/csrc/generate.cpp + the GPU Sampler of libvsmp.so (tests/generate/gen_ours);
+- ours, device-resident: vsmp::generate_device (verbo_amd/csrc/generate_device.cpp) over the same
+  double with its logits copied to the device, as an LM head on the GPU would leave them; the draw
+  stream and the history live on the device (tests/generate/gen_ours_device).
 """
 import json
 import subprocess
@@ -18,6 +21,7 @@ ROOT = Path(__file__).resolve().parents[1]
 GOLDEN = ROOT / "tests" / "golden" / "generate_golden.jsonl"
 GEN_REF = ROOT / "oracle" / "_ref" / "gen_ref"
 GEN_OURS = ROOT / "tests" / "generate" / "gen_ours"
+GEN_DEVICE = ROOT / "tests" / "generate" / "gen_ours_device"
 
 
 def _lines(text):
@@ -55,6 +59,18 @@ def test_golden_invariants():
 def test_drop_in_generate_matches_reference():
     assert GEN_OURS.is_file(), "tests/generate/gen_ours is built by __graft_entry__.build()"
     got = _lines(subprocess.run([str(GEN_OURS)], check=True, capture_output=True, text=True, timeout=120).stdout)
+    gold = _lines(GOLDEN.read_text())
+    assert [g["name"] for g in got] == [g["name"] for g in gold]
+    bad = [(a["name"], a, b) for a, b in zip(got, gold) if a != b]
+    assert not bad, bad[:2]
+
+
+@pytest.mark.gpu
+def test_device_resident_generate_matches_reference():
+    """Only the picked ids cross to the host: the sequences, Stats and text chunks still equal the
+    reference's generate scenario by scenario."""
+    assert GEN_DEVICE.is_file(), "tests/generate/gen_ours_device is built by __graft_entry__.build()"
+    got = _lines(subprocess.run([str(GEN_DEVICE)], check=True, capture_output=True, text=True, timeout=120).stdout)
     gold = _lines(GOLDEN.read_text())
     assert [g["name"] for g in got] == [g["name"] for g in gold]
     bad = [(a["name"], a, b) for a, b in zip(got, gold) if a != b]

@@ -13,10 +13,9 @@
 #include "verbo/verbo.hpp"
 #include "vsmp.h"
 #include "vsmp_error.hpp"
+#include "vsmp_internal.hpp"
 
-namespace verbo {
-
-namespace {
+namespace vsmp {
 
 std::uint64_t splitmix(std::uint64_t& s) {
   std::uint64_t z = (s += 0x9E3779B97F4A7C15ull);
@@ -24,6 +23,20 @@ std::uint64_t splitmix(std::uint64_t& s) {
   z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
   return z ^ (z >> 31);
 }
+
+void seed_stream(std::uint64_t seed, std::uint64_t out[2]) {
+  // seed 0 seeds from the clock (src/sampler.cpp:27)
+  const double us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now().time_since_epoch()).count();
+  std::uint64_t s = seed ? seed : static_cast<std::uint64_t>(us);
+  out[0] = splitmix(s);
+  out[1] = splitmix(s);
+}
+
+}  // namespace vsmp
+
+namespace verbo {
+
+namespace {
 
 struct CtxDeleter {
   void operator()(vsmp_ctx* c) const { vsmp_ctx_free(c); }
@@ -43,11 +56,7 @@ vsmp_ctx* thread_ctx() {
 Sampler::Sampler(Sampling cfg) : cfg_(cfg) { reset(); }
 
 void Sampler::reset() {
-  // seed 0 seeds from the clock (src/sampler.cpp:27)
-  const double us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now().time_since_epoch()).count();
-  std::uint64_t s = cfg_.seed ? cfg_.seed : static_cast<std::uint64_t>(us);
-  rng_[0] = splitmix(s);
-  rng_[1] = splitmix(s);
+  vsmp::seed_stream(cfg_.seed, rng_);
   hist_.clear();
 }
 

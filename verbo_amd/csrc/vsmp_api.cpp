@@ -13,6 +13,7 @@
 #include "vsmp.h"
 #include "vsmp_common.hpp"
 #include "vsmp_error.hpp"
+#include "vsmp_internal.hpp"
 
 namespace vsmp {
 
@@ -26,13 +27,13 @@ int set_error(const std::string& msg) {
 }
 void clear_error() { g_err.clear(); }
 
-namespace {
-
 bool hip_ok(hipError_t e, const char* what) {
   if (e == hipSuccess) return true;
   set_error(std::string("vsmp: ") + what + ": " + hipGetErrorString(e));
   return false;
 }
+
+namespace {
 
 // Grows a context buffer to `need` elements. `done` is the event the context records after the last
 // work of every call (calls that share a context never overlap): the old buffer is freed once it
@@ -300,8 +301,9 @@ int check_batch(const float* logits, int B, int V, long long ld, const vsmp_para
 // The kernels' arguments that do not depend on the plan or the scratch.
 KArgs batch_args(const float* logits, int B, int V, long long ld, const vsmp_params* params, int params_per_row,
                  const int* hist, const int* hist_off, int u_mode, const double* u, unsigned long long* rng_state,
-                 unsigned long long counter, int* out, const vsmp_debug* dbg) {
+                 unsigned long long counter, int* out, const vsmp_debug* dbg, const int* hist_len = nullptr) {
   KArgs a{};
+  a.hist_len = hist_len;
   a.logits = logits;
   a.ld = ld;
   a.B = B;
@@ -336,9 +338,10 @@ KArgs batch_args(const float* logits, int B, int V, long long ld, const vsmp_par
 int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
                  int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
                  unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
-                 hipStream_t st) {
+                 hipStream_t st, const int* hist_len) {
   if (check_batch(logits, B, V, ld, params, hist, hist_off, u_mode, u, rng_state, out, dbg) != 0) return -1;
-  KArgs a = batch_args(logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter, out, dbg);
+  KArgs a = batch_args(logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter, out, dbg,
+                       hist_len);
   const Plan pl = plan(ctx, B, V, params_per_row ? nullptr : params);
   const size_t slots = static_cast<size_t>(B) * static_cast<size_t>(pl.S);
   if (slots > static_cast<size_t>(INT32_MAX) / kKmax) return set_error("vsmp: batch too large");
@@ -447,16 +450,20 @@ bool mark_done(vsmp_ctx* ctx, hipStream_t st) {
   return hip_ok(hipEventRecord(ctx->done_ev, st), "hipEventRecord");
 }
 
+}  // namespace
+
 int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
                int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
                unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
-               hipStream_t st) {
+               hipStream_t st, const int* hist_len) {
   if (!ctx) return set_error("vsmp: null context");
   const int rc = launch_batch(ctx, logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
-                              out, dbg, st);
+                              out, dbg, st, hist_len);
   if (!mark_done(ctx, st)) return -1;
   return rc;
 }
+
+namespace {
 
 // vsmp_pick_batch_noalloc: row mode, one stream, the scratch in the static device array.
 int pick_batch_noalloc(const float* logits, int B, int V, long long ld, const vsmp_params* params, int params_per_row,

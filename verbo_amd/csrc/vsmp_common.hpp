@@ -33,6 +33,7 @@ struct KArgs {
   vsmp_params shared;         // the parameters of every row when params is null
   const int* hist;
   const int* hist_off;
+  const int* hist_len;  // null: row r's history ends at hist_off[r + 1]; else at hist_off[r] + hist_len[r]
   int u_mode;
   const double* u;
   unsigned long long* rng;
@@ -99,5 +100,14 @@ void launch_greedy_split(const KArgs& a, hipStream_t st);
 void launch_topk_split(const KArgs& a, hipStream_t st);
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st);
 void launch_zero_u32(uint32_t* p, long long n, hipStream_t st);
+
+// Sampler::accept (reference src/sampler.cpp:43-48) on device-resident histories: row r's history is
+// hist[off[r], off[r] + len[r]) in a region of `cap` ids. For each of the n rows that is active
+// (active null: every row), the id ids[r] (ids null: `tok`) is appended; with repeat_last > 0 a
+// history that would exceed 4 * repeat_last keeps its last repeat_last ids, as the reference trims.
+// A row whose region is full (repeat_last <= 0) appends nothing and sets *full (when not null).
+void launch_hist_accept(int* hist, const int* off, int* len, int cap, const vsmp_params* params,
+                        const vsmp_params& shared, const int* ids, int tok, const int* active, int n, int* full,
+                        hipStream_t st);
 
 }  // namespace vsmp

@@ -1,0 +1,28 @@
+// Host-side pieces shared by the library's C-ABI sources (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "vsmp.h"
+
+namespace vsmp {
+
+// false, with the calling thread's error set to "vsmp: <what>: <HIP message>", unless e is success.
+bool hip_ok(hipError_t e, const char* what);
+
+// One batched pick: the work of vsmp_pick_batch. hist_len (device-resident decode loops): row r's
+// history is hist[hist_off[r], hist_off[r] + hist_len[r]) instead of ending at hist_off[r + 1], so
+// that each row may own a region larger than its history. Returns 0 or -1 (error set).
+int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
+               int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
+               unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
+               hipStream_t st, const int* hist_len = nullptr);
+
+// verbo::Sampler's seeding (reference src/sampler.cpp:11-16,26-31): two successive SplitMix64
+// outputs of the seed; seed 0 stands for the steady clock in microseconds.
+std::uint64_t splitmix(std::uint64_t& s);
+void seed_stream(std::uint64_t seed, std::uint64_t out[2]);
+
+}  // namespace vsmp

@@ -809,7 +809,7 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
   int h0 = 0, h1 = 0;
   if (a.hist_off) {
     h0 = a.hist_off[row];
-    h1 = a.hist_off[row + 1];
+    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
   }
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
@@ -1625,7 +1625,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   int h0 = 0, h1 = 0;
   if (a.hist_off) {
     h0 = a.hist_off[row];
-    h1 = a.hist_off[row + 1];
+    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
   }
   GenCtx g;
   g.R.rp = a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld);
@@ -2130,7 +2130,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
       int h0 = 0, h1 = 0;
       if (a.hist_off) {
         h0 = a.hist_off[row];
-        h1 = a.hist_off[row + 1];
+        h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
       }
       GenRow R;
       R.rp = a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld);
@@ -2592,7 +2592,7 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   int h0 = 0, h1 = 0;
   if (a.hist_off) {
     h0 = a.hist_off[row];
-    h1 = a.hist_off[row + 1];
+    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
   }
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
@@ -2944,7 +2944,7 @@ __global__ __launch_bounds__(kTkNT) void k_topk_split(KArgs a) {
   int h0 = 0, h1 = 0;
   if (a.hist_off) {
     h0 = a.hist_off[row];
-    h1 = a.hist_off[row + 1];
+    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
   }
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
@@ -3241,7 +3241,7 @@ __global__ __launch_bounds__(kSplitNT) void k_greedy_split(KArgs a) {
   int h0 = 0, h1 = 0;
   if (a.hist_off) {
     h0 = a.hist_off[row];
-    h1 = a.hist_off[row + 1];
+    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
   }
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
@@ -3297,6 +3297,32 @@ __global__ __launch_bounds__(256) void k_read_probe(const uint4* __restrict__ p,
   if (acc == 0x9E3779B9u) sink[blockIdx.x & 7] = acc;  // keeps the loads; the value is not used
 }
 
+// Sampler::accept on device-resident histories (src/sampler.cpp:43-48), one thread per row (see
+// launch_hist_accept). The trim copies the last repeat_last - 1 ids to the front of the region (the
+// source lies at or above 3 * repeat_last + 1, past the destination) and appends the new id.
+__global__ __launch_bounds__(256) void k_hist_accept(int* __restrict__ hist, const int* __restrict__ off,
+                                                     int* __restrict__ len, int cap, const vsmp_params* params,
+                                                     vsmp_params shared, const int* ids, int tok,
+                                                     const int* active, int n, int* full) {
+  const int r = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (r >= n || (active && !active[r])) return;
+  const vsmp_params P = params ? params[r] : shared;
+  const int t = ids ? ids[r] : tok;
+  int* h = hist + off[r];
+  const int s = len[r];
+  const int keep = P.repeat_last > 0 ? P.repeat_last : 0;
+  if (keep && s + 1 > 4 * keep) {
+    for (int i = 0; i < keep - 1; ++i) h[i] = h[s + 1 - keep + i];
+    h[keep - 1] = t;
+    len[r] = keep;
+  } else if (s < cap) {
+    h[s] = t;
+    len[r] = s + 1;
+  } else if (full) {
+    *full = 1;
+  }
+}
+
 // p[0, n) = 0 (the diagnostic bitmaps, before the kernels OR into them).
 __global__ __launch_bounds__(256) void k_zero_u32(uint32_t* __restrict__ p, long long n) {
   const long long stride = static_cast<long long>(gridDim.x) * 256;
@@ -3316,6 +3342,13 @@ __global__ __launch_bounds__(256) void k_exp_probe(const double* __restrict__ x,
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st) {
   const long long blocks = std::min<long long>((n + 255) / 256, 4096);
   hipLaunchKernelGGL(k_exp_probe, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, x, y, n);
+}
+
+void launch_hist_accept(int* hist, const int* off, int* len, int cap, const vsmp_params* params,
+                        const vsmp_params& shared, const int* ids, int tok, const int* active, int n, int* full,
+                        hipStream_t st) {
+  hipLaunchKernelGGL(k_hist_accept, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, hist, off, len, cap,
+                     params, shared, ids, tok, active, n, full);
 }
 
 void launch_zero_u32(uint32_t* p, long long n, hipStream_t st) {

@@ -208,3 +208,44 @@ def make(name, rows=None):
         hist, off = _csr(hl)
         return Workload(name, lg, p, hist, off)
     raise ValueError(f"unknown workload {name!r}; one of {WORKLOADS}")
+
+
+class DecodeCase:
+    """A seeded multi-sequence decode: n sequences over a vocabulary of V, each with its own
+    sampling options (the fields of verbo_gen_opts plus repeat_last), a prompt, and next-position
+    logits that depend on the sequence, the step and the sequence's last id (so a different pick
+    changes what follows). Id 0 is the stop id; from step stop_after[r] on it gets a large bonus
+    in row r, so most sequences end on it, the others on max_tokens."""
+
+    def __init__(self, n=24, V=4096, seed=0x60):
+        self.n, self.V, self.seed = n, V, seed
+        u = uniform(seed, 0, 8 * n).reshape(n, 8)
+        self.opts = []
+        self.repeat_last = []
+        self.prompts = []
+        self.stop_after = []
+        for r in range(n):
+            self.opts.append(dict(max_tokens=8 + int(u[r, 0] * 33),
+                                  temp=(0.0, 0.5, 0.8, 1.2)[int(u[r, 1] * 4)],
+                                  top_k=(0, 20, 40, 300)[int(u[r, 2] * 4)],
+                                  top_p=(0.8, 0.95, 1.0)[int(u[r, 3] * 3)],
+                                  min_p=(0.0, 0.05)[int(u[r, 4] * 2)],
+                                  repeat=(1.0, 1.15, 1.3)[int(u[r, 5] * 3)],
+                                  seed=100 + r))
+            self.repeat_last.append((4, 16, 64)[r % 3])
+            self.prompts.append(_ints(seed + 1, r * 64, int(u[r, 6] * 31), 1, V).astype(np.int32))
+            self.stop_after.append(6 + int(u[r, 7] * 40))
+        self.stop_ids = (0,)
+
+    def logits(self, step, last):
+        """Logits [n, V] (fp32) of every sequence's next position at `step`; last[r]: row r's last
+        id (-1 before its first pick)."""
+        x = np.empty((self.n, self.V), np.float32)
+        for r in range(self.n):
+            v = 2.0 * normal(self.seed + 2 + r, step * self.V, self.V)
+            if last[r] >= 0:
+                v[(int(last[r]) * 7 + 13) % self.V] += 3.0
+            if step >= self.stop_after[r]:
+                v[0] += 6.0
+            x[r] = v.astype(np.float32)
+        return x
