@@ -23,6 +23,10 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBS = 8000.0
+# how oracle/Makefile compiles the reference's sources for the CPU baseline (its flags, stated)
+REF_BUILD = ("the reference's src/*.cpp compiled by oracle/Makefile: g++ -std=c++17 -O3 -march=x86-64-v3 -fPIC "
+             "-pthread -fvisibility=hidden -fno-math-errno (the reference's CMake flags, with x86-64-v3 for "
+             "-march=native since the library is built on another host than the one it runs on)")
 METRIC = "sampled rows/s + % HBM peak, full sampler, B=256 x V=151936 fp32 logits"
 DESCR = {
     "single": "single: 1 x 49152 fp32 N(0,2.5^2)+8 spikes, H=64, repeat 1.1, temp .7, top-k 40, top-p .9",
@@ -81,7 +85,8 @@ def cpu_baseline(w, budget):
         del lib
     out = {"value": picks / secs, "unit": "rows/s", "cores": 1, "kind": kind,
            "sample": f"{picks} pick() calls cycling over the {w.B} rows of the same workload for {secs:.1f} s, "
-                     f"1 thread, pick only (history accepted beforehand)"}
+                     f"1 thread, pick only (history accepted beforehand)",
+           "build": REF_BUILD if kind == "reference" else "oracle/vsmp_oracle.c, gcc -O2"}
     out.update(res)
     return out
 
@@ -165,7 +170,8 @@ def bench_single(args):
         O.ref_sampler_run(w.logits[0], c, w.hist, n_picks=m)
         secs = time.perf_counter() - t0
         cpu = {"value": m / secs, "unit": "draws/s", "cores": 1, "kind": "reference",
-               "sample": f"{m} consecutive pick() calls of one reference Sampler on the same row, 1 thread"}
+               "sample": f"{m} consecutive pick() calls of one reference Sampler on the same row, 1 thread",
+               "build": REF_BUILD}
     return {
         "metric": "single-row draws/s, " + DESCR["single"] + ", 10,000 consecutive draws",
         "value": 1e6 / us_eager,

@@ -114,7 +114,8 @@ VSMP_API void vsmp_ctx_free(vsmp_ctx* ctx);
 /* Batched pick over B rows of device-resident fp32 logits (row r at logits + r*ld; logits must be
  * 16-byte aligned and ld a multiple of 4, ld >= V). Replaces B independent calls of
  * verbo::Sampler::pick (reference src/sampler.cpp:50-109); there is no batched entry point in
- * the reference (its server serialises requests, cli/serve.cpp:168).
+ * the reference (its server serialises requests, cli/serve.cpp:168). V <= 1048576 (2^20): every
+ * row up to that size is exact, near-tie rows included; a larger V is rejected (-1, error text).
  *   params/params_per_row: params_per_row = 0 -> `params` is a HOST pointer to one struct used by
  *       every row; 1 -> a DEVICE array of B structs.
  *   hist/hist_off: device CSR of per-row histories, oldest first (row r = hist[hist_off[r] ..

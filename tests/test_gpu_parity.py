@@ -518,3 +518,22 @@ def test_topk_split_parts(dmode):
             st[r] = [s1[0], s1[1]]
         assert (ids == O.pick_rows(lg, p, u=u)[0]).all()
         assert (dst.cpu().numpy().view(np.uint64) == st).all()
+
+
+def test_general_path_all_rows_marked(ctx):
+    """Every row of a batch goes to the exact redo: 40 rows of 151,936 equal logits with top-p 0.5
+    (the top-p sum meets top_p exactly at an even count), a third with a penalised history, on the
+    redo's blocked sort and staged sums, in every slot at once; keep counts, ids and draw sets equal
+    the oracle's, and every row carries VSMP_FLAG_SEQ_CUTS."""
+    rng = np.random.default_rng(81)
+    B, Vv = 40, 151936
+    lg = np.zeros((B, Vv), np.float32)
+    p = V.params_array(n=B, temp=1.0, top_k=0, top_p=0.5, min_p=0.0, repeat=1.0, repeat_last=0, seed=5)
+    p["repeat"][::3] = 1.2
+    p["seed"] = rng.integers(1, 1 << 62, B)
+    h, off = csr([list(rng.integers(0, Vv, 300)) if r % 3 == 0 else [] for r in range(B)])
+    log("all rows marked", B, Vv)
+    run = Run(ctx, lg, p, h, off, cand_cap=128)
+    run.report()
+    assert (run.info["flags"] & V.FLAG_SEQ_CUTS).all(), run.info["flags"]
+    assert (run.info["keep"] == run.o_info["keep"]).all() and (run.ids == run.o_ids).all()

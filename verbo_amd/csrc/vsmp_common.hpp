@@ -17,7 +17,7 @@ constexpr int kMaxMergeSlices = 64;  // slices a small-k row may be cut into
 constexpr int kGenThreads = 1024;  // threads per general-path workgroup (one row each)
 constexpr int kGenBuckets = 4096;  // level-0 mass buckets of the general path
 constexpr int kGenCap = 1024;      // elements the general path sorts in LDS at once (power of two)
-constexpr int kMaxVocab = 1 << 26;
+constexpr int kMaxVocab = 1 << 20;  // larger rows are rejected: every accepted row can be redone exactly
 constexpr int kRowMaxVocab = 1 << 19;                    // row mode keeps the row's bitmap in LDS
 constexpr size_t kRowMaxDynLds = (kRowMaxVocab / 32) * 4;
 
@@ -59,7 +59,7 @@ struct KArgs {
   int words;                   // bitmap words per row
   // general rows whose top-p cut lay within rounding distance of top_p: k_general marks them
   // (x_flag) with the draw it used (x_u), and k_general_exact redoes them in the reference's order
-  // and sequential sums, sorting each in one of kExactSlots scratch slots of 2 * x_n entries
+  // and sequential sums, sorting each in one of exact_slots(x_n) scratch slots of 2 * x_n entries
   int* x_flag;
   double* x_u;
   unsigned long long* x_buf;
@@ -81,8 +81,14 @@ void launch_finish(const KArgs& a, hipStream_t st);
 void launch_rows(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
 void launch_general_exact(const KArgs& a, int slots, hipStream_t st);
-constexpr int kExactSlots = 8;            // workgroups (and scratch slots) of k_general_exact
-constexpr int kExactMaxVocab = 1 << 20;   // k_general_exact's reach (larger rows keep the flag)
+// Workgroups (and scratch slots of 2 * x_n entries) of k_general_exact: as many as 256 MB of slots
+// hold, between 8 and 32 (32 slots of 4 MB at 151,936 logits).
+inline int exact_slots(int x_n) {
+  const long long per = 16LL * x_n;
+  const long long n = (256LL << 20) / per;
+  return static_cast<int>(n < 8 ? 8 : (n > 32 ? 32 : n));
+}
+constexpr int kExactMaxVocab = kMaxVocab; // k_general_exact's reach: every row a call accepts
 
 // vsmp_pick_batch_noalloc: row mode only, within these limits, on one static device array per GPU
 // holding the exact redo's marks and draws (kNoAllocMaxRows each) and one sort slot (2 x 2^18

@@ -41,6 +41,12 @@ namespace {
 constexpr unsigned long long kGamma = 0x9E3779B97F4A7C15ull;
 constexpr double kTwoM53 = 1.0 / 9007199254740992.0;
 constexpr double kNearTopP = 1e-11;  // |acc - top_p| below this: reference rounding could differ
+
+// The general path's bound on that distance for a prefix of k numerators: its sums run in bucket
+// order, and a sum of k non-negative terms in any order lies within (k - 1) * 2^-53 of the exact
+// sum (relative), as does the reference's sequential one; the band is four times that, and never
+// below kNearTopP.
+__device__ __forceinline__ double near_topp(int k) { return fmax(kNearTopP, 4.0 * static_cast<double>(k) * kTwoM53); }
 constexpr double kNearMinP = 1e-13;  // |pr - thr| / thr below this: exp last-bit territory
 constexpr double kNearDraw = 1e-6;   // draws this close to a CDF boundary are reported
 
@@ -1910,9 +1916,10 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   const double u = sh.dbls[1];
   const bool topp = P.top_p > 0.0f && P.top_p < 1.0f;
   const double tp = static_cast<double>(P.top_p);
+  const double near_tp = near_topp(k);
   auto apply_topp = [&](const Sel& s) {  // src/sampler.cpp:92-100
     const double mg = fmin(fabs(s.incl / sum - tp), fabs(s.before / sum - tp));
-    if (mg < kNearTopP) flags |= VSMP_FLAG_TOPP_NEAR;
+    if (mg < near_tp) flags |= VSMP_FLAG_TOPP_NEAR;
     if (s.found && s.rank + 1 < keep) {
       keep = s.rank + 1;
       tot = s.incl;
@@ -2018,9 +2025,9 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     }
   }
   // src/sampler.cpp:92-100 can only shorten the kept set when that set holds top_p of the mass: a
-  // min-p prefix whose mass is clearly below top_p * sum (relative margin 1e-12, far above the
-  // rounding of either sum) is kept whole, and its top-p select pass is not needed
-  const bool topp_may_cut = !(tot < tp * sum * (1.0 - 1e-12));
+  // min-p prefix whose mass is clearly below top_p * sum (a relative margin of the band near_tp,
+  // far above the rounding of either sum) is kept whole, and its top-p select pass is not needed
+  const bool topp_may_cut = !(tot < tp * sum * (1.0 - near_tp));
   if (!shared && topp && topp_may_cut) apply_topp(mass_select(tp * sum));
   if (!drawn) {
     target = u * tot;
@@ -2099,17 +2106,131 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
 // ---- exact redo of general rows whose top-p cut lies at rounding distance of top_p ------------
 //
 // k_general takes the top-p cut on fp64 sums in bucket order, which decide exactly only away from
-// the boundary; a row it marks (x_flag: the cut lay within kNearTopP of top_p, as on rows of
+// the boundary; a row it marks (x_flag: the cut lay within near_topp(k) of top_p, as on rows of
 // exactly tied logits) is redone here the reference's way (src/sampler.cpp:71-108): the row's
-// composites sorted in the reference's order (value descending, index ascending) by a bitonic
-// sort in a scratch slot, the numerators, then the sums by one thread in sorted order. Workgroup w
-// owns slot w and takes rows w, w + kExactSlots, ...: each thread reads one row's mark, and the
-// marked rows are gathered in LDS and redone one after the other. Slow by design (milliseconds
-// per marked row) and rare; a call without marked rows costs one read per row.
+// composites sorted in the reference's order (value descending, index ascending) in a scratch slot,
+// the numerators, then the reference's sums in sorted order. Workgroup w owns slot w and takes rows
+// w, w + grid, ...: each thread reads one row's mark, and the marked rows are gathered in LDS and
+// redone one after the other. The sort is bitonic with every stage of stride below kXBlock run on
+// blocks held in LDS (15 global-memory stages at 2^18 composites instead of 171); the sequential
+// sums are taken by one thread from chunks staged through LDS, the quotients pr / sum of the
+// top-p sum computed by all threads (the IEEE quotient does not depend on who divides). A call
+// without marked rows costs one read per row.
+constexpr int kXBlock = 8192;  // composites the exact redo sorts or stages in LDS at once (64 KB)
+
+// One bitonic stage (size, stride) over the descending sort of xs[0, n2), by the calling workgroup.
+__device__ __forceinline__ void xsort_stage_global(uint64_t* xs, int n2, int size, int stride) {
+  for (int i = threadIdx.x; i < (n2 >> 1); i += kGenThreads) {
+    const int lo = 2 * i - (i & (stride - 1));
+    const int hi = lo + stride;
+    const bool desc = (lo & size) == 0;
+    const uint64_t x = xs[lo], y = xs[hi];
+    if ((x < y) == desc) {
+      xs[lo] = y;
+      xs[hi] = x;
+    }
+  }
+  __syncthreads();
+}
+
+// The stages (size, stride) for stride = from, from/2, ..., 1 of the blocks of kXBlock (or n2 when
+// smaller) composites of xs, each block loaded into LDS, sorted there, stored back; sizes up to
+// `size` are all taken when all_sizes. Directions follow the global index, so the network is the
+// one xsort_stage_global would run.
+__device__ void xsort_blocks(uint64_t* xs, int n2, int size, int from, bool all_sizes, uint64_t* blk) {
+  const int nb = min(n2, kXBlock);
+  for (int base = 0; base < n2; base += nb) {
+    for (int i = threadIdx.x; i < nb; i += kGenThreads) blk[i] = xs[base + i];
+    __syncthreads();
+    for (int sz = all_sizes ? 2 : size; sz <= size; sz <<= 1) {
+      for (int stride = all_sizes ? (sz >> 1) : from; stride > 0; stride >>= 1) {
+        for (int i = threadIdx.x; i < (nb >> 1); i += kGenThreads) {
+          const int lo = 2 * i - (i & (stride - 1));
+          const int hi = lo + stride;
+          const bool desc = ((base + lo) & sz) == 0;
+          const uint64_t x = blk[lo], y = blk[hi];
+          if ((x < y) == desc) {
+            blk[lo] = y;
+            blk[hi] = x;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int i = threadIdx.x; i < nb; i += kGenThreads) xs[base + i] = blk[i];
+    __syncthreads();
+  }
+}
+
+// Descending sort of xs[0, n2) (n2 a power of two): the blocks sorted in LDS, then for each larger
+// size its long-stride stages in global memory and the rest block by block in LDS.
+__device__ void xsort(uint64_t* xs, int n2, uint64_t* blk) {
+  xsort_blocks(xs, n2, min(n2, kXBlock), 0, true, blk);
+  for (int size = 2 * kXBlock; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride >= kXBlock; stride >>= 1) xsort_stage_global(xs, n2, size, stride);
+    xsort_blocks(xs, n2, size, kXBlock >> 1, false, blk);
+  }
+}
+
+constexpr int kXChunk = kXBlock - 16;  // values a chain stages at once (the reads run 16 ahead)
+
+// A sequential fp64 chain over v[0, n) in order, by thread 0, on values staged through LDS in chunks
+// of kXChunk (every thread loads a chunk, thread 0 adds it): x_{i+1} = op(x_i, f(v[i])). `stop`
+// (x_{i+1}) ends the chain at i. f runs on every thread (the staging), op only on thread 0.
+// Leaves for every thread: xo[0] the last x, xo[1] the x before it, *io the index the chain stopped
+// at (n when it did not).
+template <class F, class Op, class Stop>
+__device__ void lds_serial(const double* v, int n, double x0, F f, Op op, Stop stop, double* stage, double* xo,
+                           int* io) {
+  double x = x0, xb = x0;
+  int at = n;
+  if (threadIdx.x == 0) {
+    xo[0] = xo[1] = x0;
+    *io = n;
+  }
+  __syncthreads();
+  for (int c0 = 0; c0 < n && at == n; c0 += kXChunk) {
+    const int m = min(kXChunk, n - c0);
+    for (int i = threadIdx.x; i < m; i += kGenThreads) stage[i] = f(v[c0 + i]);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      // eight values per block, the next block's reads issued before the current block's steps
+      const double2* s2 = reinterpret_cast<const double2*>(stage);
+      double2 b0 = s2[0], b1 = s2[1], b2 = s2[2], b3 = s2[3];
+      for (int i0 = 0; i0 < m && at == n; i0 += 8) {
+        const double2* nx = s2 + (i0 >> 1) + 4;
+        const double2 n0 = nx[0], n1 = nx[1], n2 = nx[2], n3 = nx[3];
+        const double e[8] = {b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          if (i0 + t >= m || at != n) break;
+          xb = x;
+          x = op(x, e[t]);
+          if (stop(x)) at = c0 + i0 + t;
+        }
+        b0 = n0;
+        b1 = n1;
+        b2 = n2;
+        b3 = n3;
+      }
+      xo[0] = x;
+      xo[1] = xb;
+      *io = at;
+    }
+    __syncthreads();
+    at = *io;
+    __syncthreads();
+  }
+}
+
 __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
   __shared__ int list[kGenThreads];
   __shared__ int nlist;
   __shared__ int xkeep;
+  __shared__ double xd[8];
+  __shared__ int xi[4];
+  __shared__ __align__(16) uint64_t blk[kXBlock];  // sort blocks; staged chunks of the chains
+  double* stage = reinterpret_cast<double*>(blk);
   const int tid = threadIdx.x;
   const int V = a.V, n2 = a.x_n;
   uint64_t* xs = reinterpret_cast<uint64_t*>(a.x_buf) + static_cast<size_t>(blockIdx.x) * 2 * static_cast<size_t>(n2);
@@ -2157,63 +2278,54 @@ __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
       gen_pass(R, [&](int e, float v) { xs[e] = comp(ord_key(v), static_cast<uint32_t>(e)); });
       for (int i = V + tid; i < n2; i += kGenThreads) xs[i] = 0ull;
       __syncthreads();
-      for (int size = 2; size <= n2; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-          for (int i = tid; i < (n2 >> 1); i += kGenThreads) {
-            const int lo = 2 * i - (i & (stride - 1));
-            const int hi = lo + stride;
-            const bool desc = (lo & size) == 0;
-            const uint64_t x = xs[lo], y = xs[hi];
-            if ((x < y) == desc) {
-              xs[lo] = y;
-              xs[hi] = x;
-            }
-          }
-          __syncthreads();
-        }
-      }
+      xsort(xs, n2, blk);
       // src/sampler.cpp:79-83: numerators of the top-k prefix, in sorted order
       const int k = top_k_of(P, V);
       const float mx = comp_val(xs[0]);
       for (int j = tid; j < k; j += kGenThreads) pr[j] = numer(comp_val(xs[j]), mx, P.temp);
       __syncthreads();
+      const auto ident = [](double v) { return v; };
+      const auto add = [](double x, double v) { return x + v; };
+      const auto never = [](double) { return false; };
+      // src/sampler.cpp:84: the sum, sequential in sorted order
+      lds_serial(pr, k, 0.0, ident, add, never, stage, &xd[0], &xi[0]);
+      const double sum = xd[0];
+      // src/sampler.cpp:86-91: min-p, the first i >= 1 whose numerator is below thr (exact compares)
+      int keep = k;
+      if (P.min_p > 0.0f) {
+        const double thr = pr[0] * static_cast<double>(P.min_p);
+        if (tid == 0) xi[1] = k;
+        __syncthreads();
+        for (int j = 1 + tid; j < k; j += kGenThreads)
+          if (!(pr[j] >= thr)) atomicMin(&xi[1], j);
+        __syncthreads();
+        keep = xi[1];
+        __syncthreads();
+      }
+      const int keep_minp = keep;
+      // src/sampler.cpp:92-100: acc += pr[i] / sum in order; the IEEE quotients are taken by all
+      // threads, the additions by one
+      if (P.top_p > 0.0f && P.top_p < 1.0f) {
+        const double tp = static_cast<double>(P.top_p);
+        lds_serial(pr, keep, 0.0, [sum](double v) { return v / sum; }, add, [tp](double x) { return x >= tp; }, stage,
+                   &xd[2], &xi[2]);
+        const int i = xi[2];
+        if (i + 1 < keep) keep = i + 1;
+      }
+      // src/sampler.cpp:101-108: tot, then r = u * tot minus the numerators in order, first r <= 0
+      lds_serial(pr, keep, 0.0, ident, add, never, stage, &xd[4], &xi[3]);
+      const double tot = xd[4];
+      const double u = a.x_u[row];
+      const double r0 = u * tot;
+      lds_serial(pr, keep, r0, ident, [](double x, double v) { return x - v; }, [](double x) { return x <= 0.0; }, stage,
+                 &xd[6], &xi[0]);
+      const int f = xi[0];
+      const bool picked = f < keep;
+      const int pick = picked ? f : keep - 1;
       if (tid == 0) {
-        double sum = 0.0;  // src/sampler.cpp:84
-        for (int j = 0; j < k; ++j) sum += pr[j];
-        int keep = k;  // src/sampler.cpp:86-91
-        if (P.min_p > 0.0f) {
-          const double thr = pr[0] * static_cast<double>(P.min_p);
-          keep = 1;
-          while (keep < k && pr[keep] >= thr) ++keep;
-        }
-        const int keep_minp = keep;
-        if (P.top_p > 0.0f && P.top_p < 1.0f) {  // src/sampler.cpp:92-100
-          const double tp = static_cast<double>(P.top_p);
-          double acc = 0.0;
-          int i = 0;
-          for (; i < keep; ++i) {
-            acc += pr[i] / sum;
-            if (acc >= tp) break;
-          }
-          if (i + 1 < keep) keep = i + 1;
-        }
-        double tot = 0.0;  // src/sampler.cpp:101-108
-        for (int j = 0; j < keep; ++j) tot += pr[j];
-        const double u = a.x_u[row];
-        double r = u * tot, before = r;
-        int pick = keep - 1;
-        bool picked = false;
-        for (int j = 0; j < keep; ++j) {
-          before = r;
-          r -= pr[j];
-          if (r <= 0.0) {
-            pick = j;
-            picked = true;
-            break;
-          }
-        }
-        double mg = fabs(r);
-        if (picked && pick > 0 && before < mg) mg = before;
+        double mg = fabs(xd[6]);                          // the remainder that crossed (or the last one)
+        if (picked && pick > 0 && xd[7] < mg) mg = xd[7];  // and the one before it
+
         const int id = comp_idx(xs[pick]);
         a.out[row] = id;
         if (a.info) {
@@ -3134,6 +3246,12 @@ __global__ __launch_bounds__(kTkNT) void k_topk_split(KArgs a) {
   }
   __syncthreads();
   if (!sh.ints[9]) return;
+  // The last part: every other part's lists and counts were stored with agent-scope stores
+  // (written through to the memory side, past the XCDs' L2s) and had completed (vmcnt(0)) before
+  // that part's ticket; the ticket's read-modify-write, performed at the memory side, returned P - 1
+  // to this part only after all of them; the merge reads them with agent-scope loads, which bypass
+  // the L2 as well. An acquire fence here (buffer_inv sc1: the XCD's L2 dropped) added 1.5-3.7 us at
+  // 1-24 rows of 151,936 (the other parts' data leaving that L2) and is not taken.
   if (tid == 0) __hip_atomic_store(&a.g_tick[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   finish_smallk<kTkNT, true>(a, row, P, a.P, sh.mbuf, sh.top, sh.red64, sh.ints, sh.off);
 }
@@ -3265,6 +3383,7 @@ __global__ __launch_bounds__(kSplitNT) void k_greedy_split(KArgs a) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     const unsigned t = __hip_atomic_fetch_add(&a.g_tick[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t == static_cast<unsigned>(a.P - 1)) {  // the last part: every part's maximum is in the slot
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // one fence per row, in its last part only
       const uint64_t b = __hip_atomic_exchange(&a.g_slot[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const uint32_t npr = a.info ? __hip_atomic_exchange(&a.g_npen[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
       __hip_atomic_store(&a.g_tick[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
