@@ -1382,9 +1382,31 @@ __device__ __forceinline__ double numer_g(const GenCtx& g, float v) {
   return exp_tab(static_cast<double>(v - g.mx) * g.inv_temp);
 }
 
-__device__ __forceinline__ int q_of(const GenCtx& g, float v) {
-  const float t = (g.mx - v) * g.qs;
-  return t < static_cast<float>(kGenBuckets) ? static_cast<int>(t) : kGenBuckets - 1;
+// Level-0 bucket of an element from d = v - mx (as the numerator takes it): t = -d * qs, which is
+// (mx - v) * qs bit for bit (rounding to nearest is symmetric), truncated; t >= kGenBuckets, +inf
+// and NaN all give the last bucket.
+__device__ __forceinline__ int q_of_d(const GenCtx& g, float d) {
+  return static_cast<int>(fminf(-d * g.qs, static_cast<float>(kGenBuckets) - 0.5f));
+}
+__device__ __forceinline__ int q_of(const GenCtx& g, float v) { return q_of_d(g, v - g.mx); }
+
+// The main pass's numerator exp(double(d) / temp) by a table over bucket pairs: buckets 2j and
+// 2j + 1 share the point c_j = -(2j + 1) w, w = 1 / (qs temp) (one bucket's width in exponent
+// units; the buckets reach at most 64 temp below the maximum, so w <= 1/64), etab[j] = exp(c_j).
+// For an element of bucket q, x = double(d) / temp lies within w of c_(q >> 1) (up to the float
+// rounding of the bucket index), and exp(x - c_j) is its degree-6 Taylor polynomial (truncation
+// below 4.4e-17). About 13 instructions against exp_tab's 18. Valid below the last bucket, and in
+// it when the buckets reach the row minimum.
+__device__ __forceinline__ double numer_tab(const GenCtx& g, const double* etab, double w, float d, int q) {
+  const double x = static_cast<double>(d) * g.inv_temp;
+  const double r = fma(static_cast<double>(q | 1), w, x);
+  double s = fma(r, 0x1.6c16c16c16c17p-10, 0x1.1111111111111p-7);  // 1/720, 1/120
+  s = fma(r, s, 0x1.5555555555555p-5);                              // 1/24
+  s = fma(r, s, 0x1.5555555555555p-3);                              // 1/6
+  s = fma(r, s, 0.5);
+  s = fma(r, s, 1.0);
+  const double e = etab[q >> 1];
+  return fma(e * r, s, e);
 }
 
 // atomicMin(dst, i) for the lane of this wave whose claim holds with the smallest lane index (the
@@ -1718,47 +1740,66 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     sh.cnt0[i] = 0u;
     sh.mass0[i] = 0.0;
   }
+  // the main pass's table (numer_tab), in the refinement histograms, which are free until it ends
+  double* etab = sh.rmass;
+  const double wq = g.qs > 0.0f ? 1.0 / (static_cast<double>(g.qs) * static_cast<double>(P.temp)) : 0.0;
+  for (int j = tid; j < kGenBuckets / 2; j += kGenThreads) etab[j] = exp_tab(-static_cast<double>(2 * j + 1) * wq);
   __syncthreads();
   const bool minp = P.min_p > 0.0f;
   const double thr = static_cast<double>(P.min_p);  // pr of the maximum is exactly 1
   double t_sum = 0.0, t_totm = 0.0, t_omass = 0.0;
   uint32_t t_cntm = 0, t_ocnt = 0;
   const bool cut_k = g.ckk != 0ull;
-  // ovf: the overflow bucket (most of a cold row when capped) is summed per thread rather than by
+  // The overflow bucket of a capped row holds elements at least 63.98 temp below the maximum, whose
+  // numerators are below 1.6e-28: together under 2e-22 of the sum (the maximum's numerator is 1),
+  // which a sum in the reference's order absorbs without a trace. They are counted without a
+  // numerator, unless a min-p threshold that small could keep them (then exp_tab gives theirs).
+  const bool ovf_exact = capped && minp && thr < 1e-26;
+  // ovf: the overflow bucket (most of a cold row when capped) is counted per thread rather than by
   // atomics that would all hit one address; with_minp: the min-p statistics are taken
   auto main_pass = [&](auto ovf, auto with_minp, auto with_cut) {
     auto excluded = [&](int e, float v) {
       return decltype(with_cut)::value && cut_k && comp(ord_key(v), static_cast<uint32_t>(e)) < g.ckk;
     };
-    auto add = [&](float v, double p) {
-      t_sum += p;
-      if (decltype(with_minp)::value && minp && p >= thr) {
-        ++t_cntm;
-        t_totm += p;
-      }
-      const int q = q_of(g, v);
+    auto add = [&](float v, int q, double p) {
       if (decltype(ovf)::value && q == kGenBuckets - 1) {
         ++t_ocnt;
+        if (capped) {
+          if (!ovf_exact) return;
+          p = numer_g(g, v);
+        }
         t_omass += p;
       } else {
         atomicAdd(&sh.cnt0[q], 1u);
         atomicAdd(&sh.mass0[q], p);
       }
+      t_sum += p;
+      if (decltype(with_minp)::value && minp && p >= thr) {
+        ++t_cntm;
+        t_totm += p;
+      }
     };
     gen_pass_groups<1>(
         g.R,
         [&](int e, float v) {
-          if (!excluded(e, v)) add(v, numer_g(g, v));
+          const float d = v - g.mx;
+          const int q = q_of_d(g, d);
+          if (!excluded(e, v)) add(v, q, numer_tab(g, etab, wq, d, q));
         },
-        // the four numerators first: their exp-table reads then go out together, ahead of the
+        // the four numerators first: their table reads then go out together, ahead of the
         // histogram atomics (LDS writes, which later LDS reads may not pass)
         [&](int e, const float (&x)[4]) {
+          int q[4];
           double p[4];
 #pragma unroll
-          for (int c = 0; c < 4; ++c) p[c] = numer_g(g, x[c]);
+          for (int c = 0; c < 4; ++c) {
+            const float d = x[c] - g.mx;
+            q[c] = q_of_d(g, d);
+            p[c] = numer_tab(g, etab, wq, d, q[c]);
+          }
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            if (!excluded(e + c, x[c])) add(x[c], p[c]);
+            if (!excluded(e + c, x[c])) add(x[c], q[c], p[c]);
         });
   };
   // one instance per combination without a top-k restriction (the common case: no per-element
