@@ -164,6 +164,12 @@ VSMP_API int vsmp_read_probe(vsmp_ctx* ctx, const void* p, long long bytes, void
  * above 256) uses for its numerators, for i < n, on `stream` (x, y: device arrays of n doubles).
  * Its accuracy against exp is what the tests bound. Returns 0 or -1. */
 VSMP_API int vsmp_exp_probe(vsmp_ctx* ctx, const double* x, double* y, long long n, void* stream);
+/* Diagnostics, no reference counterpart: y[i] = the numerator exp(double(d[i]) / temp) as the
+ * general path's main pass takes it (a table over its level-0 buckets, scale qs = 4096 / span, the
+ * span at most 64 temp), for d[i] = v - max <= 0 within the span, i < n (d: device floats, y:
+ * device doubles). Its accuracy against exp is what the tests bound. Returns 0 or -1. */
+VSMP_API int vsmp_numer_probe(vsmp_ctx* ctx, const float* d, double* y, long long n, float temp, float qs,
+                              void* stream);
 
 /* A drop-in sampler object: verbo::Sampler (reference include/verbo/verbo.hpp:116-132) behind
  * a C handle, for FFI callers. Its history, xorshift stream and seeding are the reference's

@@ -353,6 +353,35 @@ def test_general_path_exp_accuracy(ctx):
     assert special.tolist() == [0.0, 0.0, 0.0]
 
 
+@pytest.mark.parametrize("span", [64.0, 20.0, 3.0, 1e-3])
+def test_general_path_table_numerator_accuracy(ctx, span):
+    """The main pass's numerators (a table over its bucket pairs and a degree-6 polynomial) against
+    exp(d / temp) in long double, for the bucket scales of rows whose span is 64 temp (the widest,
+    bucket width 1/64 in exponent units), 20, 3 and 1e-3 temp: relative error within
+    (2.5 + |x|) * 2^-52, x = d / temp: 2.5 units of the exp itself, and |x| * 2^-52 for the exponent,
+    which the path forms as d * (1 / temp) where the reference divides (exact at temp 1, where the
+    bound is 2.5 * 2^-52 alone). Elements over the whole span and at every bucket edge (where the
+    float bucket index rounds); 1 within an ulp at d = 0."""
+    import torch
+
+    rng = np.random.default_rng(31)
+    for temp in (1.0, 0.37, 1.9):
+        qs = np.float32(4096.0 / (span * temp))
+        edges = -(np.arange(4097, dtype=np.float64) / np.float64(qs))
+        d = np.concatenate([-np.float64(span * temp) * rng.random(400000), edges, np.nextafter(edges, 0.0),
+                            np.nextafter(edges, -np.inf), [0.0, -0.0]]).astype(np.float32)
+        d = d[(d <= 0) & (d >= -np.float32(span * temp) * np.float32(0.99999))]
+        y = ctx.numer_probe(torch.from_numpy(d).cuda(), temp, float(qs)).cpu().numpy()
+        x = d.astype(np.longdouble) / np.longdouble(np.float32(temp))
+        ref = np.exp(x)
+        rel = np.abs(y.astype(np.longdouble) - ref) / ref / np.longdouble(2.0**-52)
+        bound = 2.5 + (np.abs(x) if temp != 1.0 else 0.0)
+        worst = int(np.argmax(rel - bound))
+        assert rel[worst] <= bound if np.ndim(bound) == 0 else rel[worst] <= bound[worst], \
+            (span, temp, float(d[worst]), y[worst], float(ref[worst]), float(rel[worst]))
+        assert abs(y[d == 0][0] - 1.0) <= 2.3e-16
+
+
 @pytest.mark.parametrize("dmode", ["split", "rows"])
 def test_greedy_split_parts(dmode):
     """Greedy batches cut into parts (one launch, the last part of a row writes its id) against the

@@ -137,6 +137,7 @@ def load_library():
         "vsmp_sampler_reset": (None, [_P]),
         "vsmp_read_probe": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P]),
         "vsmp_exp_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_longlong, _P]),
+        "vsmp_numer_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_longlong, ctypes.c_float, ctypes.c_float, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -305,6 +306,21 @@ class Context:
         y = torch.empty_like(x)
         st = stream if stream is not None else torch.cuda.current_stream(x.device)
         if _lib.vsmp_exp_probe(self._h, x.data_ptr(), y.data_ptr(), x.numel(), ctypes.c_void_p(st.cuda_stream)) != 0:
+            raise _err()
+        return y
+
+    def numer_probe(self, d, temp, qs, stream=None):
+        """vsmp_numer_probe: the main pass's numerators exp(double(d) / temp) for float32 device
+        tensor `d` (= v - max <= 0), buckets of scale qs; returns float64 y."""
+        import torch
+
+        if d.dtype != torch.float32 or not d.is_cuda:
+            raise VsmpError("numer_probe needs a float32 device tensor")
+        d = d.contiguous()
+        y = torch.empty(d.shape, dtype=torch.float64, device=d.device)
+        st = stream if stream is not None else torch.cuda.current_stream(d.device)
+        if _lib.vsmp_numer_probe(self._h, d.data_ptr(), y.data_ptr(), d.numel(), float(temp), float(qs),
+                                 ctypes.c_void_p(st.cuda_stream)) != 0:
             raise _err()
         return y
 

@@ -81,6 +81,7 @@ void launch_finish(const KArgs& a, hipStream_t st);
 void launch_rows(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
 void launch_general_exact(const KArgs& a, int slots, hipStream_t st);
+void launch_numer_probe(const float* d, double* y, long long n, float temp, float qs, hipStream_t st);
 // Workgroups (and scratch slots of 2 * x_n entries) of k_general_exact: as many as 256 MB of slots
 // hold, between 8 and 32 (32 slots of 4 MB at 151,936 logits).
 inline int exact_slots(int x_n) {

@@ -28,6 +28,7 @@
 //            top_p) redone in the reference's order and sequential sums.
 //  k_read_probe  a plain streaming read, for the attainable-bandwidth measurement.
 //  k_exp_probe   the general path's fp64 exp over an array, for measuring its accuracy.
+//  k_numer_probe the main pass's table numerators over an array, for measuring their accuracy.
 #include <algorithm>
 #include <cfloat>
 #include <mutex>
@@ -1397,6 +1398,14 @@ __device__ __forceinline__ int q_of(const GenCtx& g, float v) { return q_of_d(g,
 // rounding of the bucket index), and exp(x - c_j) is its degree-6 Taylor polynomial (truncation
 // below 4.4e-17). About 13 instructions against exp_tab's 18. Valid below the last bucket, and in
 // it when the buckets reach the row minimum.
+// The table's spacing w: one bucket's width, 1 / (qs temp), kept to 41 significant bits so that
+// every table point (2j + 1) w, j < 2048, is exact in fp64 (numer_tab then subtracts exactly the
+// point whose exp the table holds).
+__device__ __forceinline__ double table_width(float qs, float temp) {
+  if (!(qs > 0.0f)) return 0.0;
+  const double w = 1.0 / (static_cast<double>(qs) * static_cast<double>(temp));
+  return __longlong_as_double(__double_as_longlong(w) & ~0xFFFll);
+}
 __device__ __forceinline__ double numer_tab(const GenCtx& g, const double* etab, double w, float d, int q) {
   const double x = static_cast<double>(d) * g.inv_temp;
   const double r = fma(static_cast<double>(q | 1), w, x);
@@ -1742,7 +1751,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   }
   // the main pass's table (numer_tab), in the refinement histograms, which are free until it ends
   double* etab = sh.rmass;
-  const double wq = g.qs > 0.0f ? 1.0 / (static_cast<double>(g.qs) * static_cast<double>(P.temp)) : 0.0;
+  const double wq = table_width(g.qs, P.temp);
   for (int j = tid; j < kGenBuckets / 2; j += kGenThreads) etab[j] = exp_tab(-static_cast<double>(2 * j + 1) * wq);
   __syncthreads();
   const bool minp = P.min_p > 0.0f;
@@ -3497,7 +3506,31 @@ __global__ __launch_bounds__(256) void k_exp_probe(const double* __restrict__ x,
   for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) y[i] = exp_tab(x[i]);
 }
 
+// Diagnostics: y[i] = the main pass's numerator (numer_tab) of an element at d[i] = v - mx below the
+// row maximum, for buckets of scale qs and temperature temp, as the main pass places them.
+__global__ __launch_bounds__(256) void k_numer_probe(const float* __restrict__ d, double* __restrict__ y, long long n,
+                                                     float temp, float qs) {
+  __shared__ double etab[kGenBuckets / 2];
+  exp_tab_fill();
+  __syncthreads();
+  GenCtx g{};
+  g.temp = temp;
+  g.inv_temp = 1.0 / static_cast<double>(temp);
+  g.qs = qs;
+  const double wq = table_width(qs, temp);
+  for (int j = threadIdx.x; j < kGenBuckets / 2; j += 256) etab[j] = exp_tab(-static_cast<double>(2 * j + 1) * wq);
+  __syncthreads();
+  const long long stride = static_cast<long long>(gridDim.x) * 256;
+  for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+    y[i] = numer_tab(g, etab, wq, d[i], max(q_of_d(g, d[i]), 0));  // d > 0 (no row holds one) kept in range
+}
+
 }  // namespace
+
+void launch_numer_probe(const float* d, double* y, long long n, float temp, float qs, hipStream_t st) {
+  const long long blocks = std::min<long long>((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(k_numer_probe, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, d, y, n, temp, qs);
+}
 
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st) {
   const long long blocks = std::min<long long>((n + 255) / 256, 4096);
