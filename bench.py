@@ -213,6 +213,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0: skip)")
     ap.add_argument("--min-buffer-mb", type=float, default=640.0)
     ap.add_argument("--draws", type=int, default=10000, help="single workload: consecutive draws timed")
+    ap.add_argument("--eager", action="store_true", help="issue the timed calls one by one instead of from a HIP graph")
     ap.add_argument("--copy", action="store_true",
                     help="time a plain device copy of one logits buffer per step instead (the known-size kernel "
                          "that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -248,31 +249,56 @@ def main():
     ctx = V.Context(0)
     stream = torch.cuda.current_stream(dev)
 
-    def step(i):
-        ctx.pick_batch(bufs[i % nbuf], params, hist, hoff, V.U_COUNTER, counter=i, out=out, stream=stream)
+    def step(i, st=stream):
+        ctx.pick_batch(bufs[i % nbuf], params, hist, hoff, V.U_COUNTER, counter=i, out=out, stream=st)
 
     if args.copy:
         dst = torch.empty_like(bufs[0])
 
-        def step(i):  # noqa: F811 - the calibration step replaces the sampler step
+        def step(i, st=stream):  # noqa: F811 - the calibration step replaces the sampler step
             dst.copy_(bufs[i % nbuf])
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done, {nbuf} buffers x {nbytes / 1e6:.1f} MB")
-    # two events bracket the timed steps on the launch stream: nothing is inserted between launches
+    # The K timed steps are issued from a HIP graph that holds them (captured once, replayed once):
+    # the GPU then runs them back to back, and the figure is the sampler's, not the Python loop's
+    # launch rate (each call costs the host tens of microseconds in ctypes and planning). Two
+    # events bracket the replay on the launch stream. --eager times the calls issued one by one.
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    use_graph = not (args.eager or args.copy)
+    if use_graph:
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream(dev)
+        cap.wait_stream(stream)
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(args.steps):
+                step(args.warmup + i, cap)
+        torch.cuda.synchronize()
+        graph.replay()  # untimed: the first replay uploads the graph
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     e0.record(stream)
-    for i in range(args.steps):
-        step(args.warmup + i)
+    if use_graph:
+        graph.replay()
+    else:
+        for i in range(args.steps):
+            step(args.warmup + i)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     total_ms = e0.elapsed_time(e1)
     ms_per_step = total_ms / args.steps
+    eager_ms = None
+    if use_graph:  # the same steps issued one by one, for comparison
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(args.steps):
+            step(args.warmup + i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        eager_ms = e0.elapsed_time(e1) / args.steps
     log(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (wall {wall * 1e3:.2f} ms)")
     if args.copy:
         gbs = 2 * nbytes / (ms_per_step * 1e-3) / 1e9
@@ -309,7 +335,9 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": DESCR[args.workload], "B": w.B, "V": w.V, "buffers": nbuf,
-                   "algorithmic_bytes_per_step": alg, "epilogue_dtype": "f64"},
+                   "algorithmic_bytes_per_step": alg, "epilogue_dtype": "f64",
+                   "issue": "hip_graph" if use_graph else "eager",
+                   "eager_ms_per_step": eager_ms},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "attainable_read": attainable},
     }
