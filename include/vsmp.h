@@ -147,6 +147,39 @@ VSMP_API int vsmp_pick_batch_noalloc(const float* logits, int B, int V, long lon
                                      unsigned long long* rng_state, unsigned long long counter,
                                      int* out, const vsmp_debug* dbg, void* stream);
 
+/* The LM head alone: logits[r][c] = sum_d hidden[r][d] * head[c][d] for r < B, c < V, on `stream`.
+ * The product of the reference's Session (src/session.cpp:169, matmul(m->head, ...)) on the GPU:
+ * hidden (the final norm's output, B rows of D) and head (V rows of D) are bfloat16 bit patterns
+ * (uint16), accumulated in fp32 on the matrix cores; every logit is computed in the same order
+ * whatever the batch, so it is also the value vsmp_head_pick samples from.
+ *   hidden: device bf16 [B][ldh]; head: device bf16 [V][ldw]; both 16-byte aligned, ldh and ldw
+ *       multiples of 8 and >= D; D a multiple of 64 in [64, 16384]; V <= 524288 (2^19).
+ *   logits: device fp32 [B][ldl], ldl >= V.
+ * Returns 0 or -1. */
+VSMP_API int vsmp_head_logits(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head,
+                              long long ldw, int B, int V, int D, float* logits, long long ldl,
+                              void* stream);
+
+/* The LM head and the pick in one call: the ids vsmp_pick_batch would pick from the logits that
+ * vsmp_head_logits writes, without writing them. Replaces Session's head product
+ * (src/session.cpp:169) followed by Sampler::pick (src/sampler.cpp:50-109) on its row; the
+ * reference has no such fused call. Greedy and small-k rows (temp <= 0, or 0 < top_k <= 256)
+ * keep only the columns whose logit reaches a per-row bound (the k-th largest penalised logit of
+ * the first 4096 columns) and never write their logits; other rows (top-k off or above 256) are
+ * written whole and sampled by the general path.
+ *   hidden, head, B, V, D, ldh, ldw: as vsmp_head_logits.
+ *   params ... dbg: as vsmp_pick_batch.
+ *   logits/ldl: NULL, or a device fp32 [B][ldl] output that receives every row's logits too
+ *       (16-byte aligned, ldl >= V and a multiple of 4).
+ * Scratch (in the context): B x V candidate composites (8 bytes each), and B x V fp32 logits when
+ * rows may take the general path and `logits` is NULL. Returns 0 or -1. */
+VSMP_API int vsmp_head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head,
+                            long long ldw, int B, int V, int D, const vsmp_params* params,
+                            int params_per_row, const int* hist, const int* hist_off, int u_mode,
+                            const double* u, unsigned long long* rng_state,
+                            unsigned long long counter, int* out, float* logits, long long ldl,
+                            const vsmp_debug* dbg, void* stream);
+
 /* One pick on a HOST logits row with a host history and a supplied draw u: the computation of
  * verbo::Sampler::pick(logits, n) (reference src/sampler.cpp:50-109) for a sampler whose history
  * is hist[0..H) and whose next stream draw is u. Copies the row to the device, runs the kernels

@@ -60,7 +60,11 @@ def csr(hists):
 class Run:
     """One batched GPU pick and the oracle's answer on the same inputs."""
 
-    def __init__(self, ctx, logits, params, hist=None, hist_off=None, u=None, cand_cap=128, ld=None, device="cuda"):
+    def __init__(self, ctx, logits, params, hist=None, hist_off=None, u=None, cand_cap=128, ld=None, device="cuda",
+                 pick=None):
+        """pick: None (ctx.pick_batch on the logits, uploaded), or a callable taking pick_batch's
+        arguments (params, hist, hist_off, u and the diagnostic tensors as keywords) that makes the
+        same pick some other way (the LM-head path, whose `logits` are the head's own output)."""
         import torch
 
         self.logits = np.ascontiguousarray(logits, np.float32)
@@ -89,8 +93,11 @@ class Run:
         pen = torch.full((B, (Vv + 31) // 32), -1, dtype=torch.int32, device=device)
         pr = V.Params(*[self.params[0][f].item() for f in V.SAMPLING_DTYPE.names]) if not per_row else \
             V.to_device_params(self.params, device)
-        out = ctx.pick_batch(_rows_view(dl), pr, dh, dho, V.U_SUPPLIED, du, info=info, cand_ids=cid, cand_pr=cpr,
-                             pen_bits=pen)
+        if pick is None:
+            out = ctx.pick_batch(_rows_view(dl), pr, dh, dho, V.U_SUPPLIED, du, info=info, cand_ids=cid, cand_pr=cpr,
+                                 pen_bits=pen)
+        else:
+            out = pick(pr, dh, dho, du, info=info, cand_ids=cid, cand_pr=cpr, pen_bits=pen)
         torch.cuda.synchronize()
         self.ids = out.cpu().numpy()
         self.info = V.row_info(info)

@@ -138,6 +138,11 @@ def load_library():
         "vsmp_read_probe": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P]),
         "vsmp_exp_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_longlong, _P]),
         "vsmp_numer_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_longlong, ctypes.c_float, ctypes.c_float, _P]),
+        "vsmp_head_logits": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P, ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, _P, ctypes.c_longlong, _P]),
+        "vsmp_head_pick": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P, ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, _P, ctypes.c_int, _P, _P, ctypes.c_int, _P, _P,
+                                          ctypes.c_ulonglong, _P, _P, ctypes.c_longlong, ctypes.POINTER(Debug), _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -253,6 +258,22 @@ def pick_batch_noalloc(logits, params, hist=None, hist_off=None, u_mode=U_COUNTE
     return out
 
 
+def _check_rows(t, dtype, name):
+    if not t.is_cuda or t.dtype != dtype or t.dim() != 2 or t.stride(1) != 1:
+        raise VsmpError(f"{name} must be a 2-D {dtype} device tensor with contiguous rows")
+
+
+def _head_shapes(hidden, head):
+    """(B, D, V) of a head call on bf16 device tensors hidden [B, D] and head [V, D]."""
+    import torch
+
+    _check_rows(hidden, torch.bfloat16, "hidden")
+    _check_rows(head, torch.bfloat16, "head")
+    if hidden.shape[1] != head.shape[1]:
+        raise VsmpError("hidden and head must have the same number of columns (D)")
+    return hidden.shape[0], hidden.shape[1], head.shape[0]
+
+
 class Context:
     """A vsmp_ctx on one device: scratch for batched picks, staging for host picks."""
 
@@ -284,6 +305,56 @@ class Context:
         if _lib.vsmp_pick_batch(self._h, *args) != 0:
             raise _err()
         del keep
+        return out
+
+    def head_logits(self, hidden, head, logits=None, stream=None):
+        """vsmp_head_logits: logits = hidden @ head.T for bf16 device tensors hidden [B, D] and head
+        [V, D] (rows contiguous), fp32 accumulation; returns logits (float32 [B, V] unless given)."""
+        import torch
+
+        B, D, V = _head_shapes(hidden, head)
+        if logits is None:  # rows padded to 16 bytes, so that pick_batch can take them
+            logits = torch.empty(B, (V + 3) // 4 * 4, dtype=torch.float32, device=hidden.device)[:, :V]
+        _check_rows(logits, torch.float32, "logits")
+        st = stream if stream is not None else torch.cuda.current_stream(hidden.device)
+        if _lib.vsmp_head_logits(self._h, hidden.data_ptr(), hidden.stride(0), head.data_ptr(), head.stride(0), B, V, D,
+                                 logits.data_ptr(), logits.stride(0), ctypes.c_void_p(st.cuda_stream)) != 0:
+            raise _err()
+        return logits
+
+    def head_pick(self, hidden, head, params, hist=None, hist_off=None, u_mode=U_COUNTER, u=None, rng_state=None,
+                  counter=0, out=None, logits=None, info=None, cand_ids=None, cand_pr=None, pen_bits=None, stream=None):
+        """vsmp_head_pick: the head's product and pick_batch's pick in one call (the ids pick_batch
+        takes from head_logits' logits). `logits`: None, or a float32 [B, >= V] device tensor that
+        receives the logits as well. The rest as pick_batch. Returns `out` (int32 [B])."""
+        import torch
+
+        B, D, V = _head_shapes(hidden, head)
+        if out is None:
+            out = torch.empty(B, dtype=torch.int32, device=hidden.device)
+        if logits is not None:
+            _check_rows(logits, torch.float32, "logits")
+        if isinstance(params, Params):
+            pp, per_row = ctypes.addressof(params), 0
+        else:
+            if params.numel() != 32 * B:
+                raise VsmpError("per-row params must hold B entries")
+            pp, per_row = _addr(params), 1
+        cap = cand_ids.shape[1] if cand_ids is not None else 0
+        if pen_bits is not None and pen_bits.numel() != B * ((V + 31) // 32):
+            raise VsmpError("pen_bits must hold B * ceil(V / 32) words")
+        dbg = None
+        if info is not None or cand_ids is not None or pen_bits is not None:
+            dbg = Debug(_addr(info), _addr(cand_ids), _addr(cand_pr), cap, _addr(pen_bits))
+        st = stream if stream is not None else torch.cuda.current_stream(hidden.device)
+        rc = _lib.vsmp_head_pick(self._h, hidden.data_ptr(), hidden.stride(0), head.data_ptr(), head.stride(0), B, V, D,
+                                 pp, per_row, _addr(hist), _addr(hist_off), int(u_mode), _addr(u), _addr(rng_state),
+                                 int(counter), _addr(out), logits.data_ptr() if logits is not None else None,
+                                 logits.stride(0) if logits is not None else 0,
+                                 ctypes.byref(dbg) if dbg is not None else None, ctypes.c_void_p(st.cuda_stream))
+        if rc != 0:
+            raise _err()
+        del params, dbg
         return out
 
     def read_probe(self, t, stream=None):

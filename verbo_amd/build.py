@@ -16,7 +16,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libvsmp.so"
-SOURCES = ["vsmp_kernels.hip", "vsmp_api.cpp", "sampler.cpp", "decode.cpp"]
+SOURCES = ["vsmp_kernels.hip", "vsmp_head.hip", "vsmp_api.cpp", "sampler.cpp", "decode.cpp"]
 ARCH = os.environ.get("VSMP_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the device code.

@@ -110,6 +110,20 @@ struct vsmp_ctx {
   size_t n_tick = 0;
   unsigned int* g_npen = nullptr;
   size_t n_gnpen = 0;
+  // LM-head path (vsmp_head_pick): probe logits, row bounds and modes, candidate lists, and the
+  // logits of rows that are written whole (general rows) when the caller keeps none
+  float* h_probe = nullptr;
+  size_t n_probe = 0;
+  float* h_full = nullptr;
+  size_t n_full = 0;
+  unsigned int* h_tk = nullptr;
+  size_t n_tk = 0;
+  unsigned char* h_rmode = nullptr;
+  size_t n_rmode = 0;
+  int* h_cnt = nullptr;
+  size_t n_hcnt = 0;
+  unsigned long long* h_cand = nullptr;
+  size_t n_hcand = 0;
   // host-pointer path buffers
   float* d_logits = nullptr;
   size_t n_logits = 0;
@@ -466,6 +480,156 @@ int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, c
 
 namespace {
 
+// ---- the LM head: vsmp_head_logits, vsmp_head_pick ------------------------------------------------
+
+// logits_rows16: the logits are also read by the sampler's kernels (16-byte aligned rows)
+int check_head(const void* hidden, long long ldh, const void* head, long long ldw, int B, int V, int D,
+               const float* logits, long long ldl, bool logits_rows16) {
+  if (!hidden || !head) return set_error("vsmp: hidden and head are required");
+  if (B < 1 || V < 1) return set_error("vsmp: need B >= 1 and V >= 1");
+  if (V > kHeadMaxVocab) return set_error("vsmp: the head path takes at most " + std::to_string(kHeadMaxVocab) + " columns");
+  if (D < kHeadKC || D % kHeadKC != 0 || D > kHeadMaxD)
+    return set_error("vsmp: D must be a multiple of " + std::to_string(kHeadKC) + " in [" + std::to_string(kHeadKC) + ", " +
+                     std::to_string(kHeadMaxD) + "]");
+  if (ldh < D || ldw < D || ldh % 8 != 0 || ldw % 8 != 0)
+    return set_error("vsmp: ldh and ldw must be >= D and multiples of 8 (16-byte rows)");
+  if (((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(head)) & 15u) != 0)
+    return set_error("vsmp: hidden and head must be 16-byte aligned");
+  if (logits && ldl < V) return set_error("vsmp: ldl must be >= V");
+  if (logits && logits_rows16 && ((ldl & 3) != 0 || (reinterpret_cast<uintptr_t>(logits) & 15u) != 0))
+    return set_error("vsmp: logits must be 16-byte aligned with ldl a multiple of 4");
+  return 0;
+}
+
+HeadArgs head_args(const void* hidden, long long ldh, const void* head, long long ldw, int B, int V, int D) {
+  HeadArgs h{};
+  h.x = static_cast<const uint16_t*>(hidden);
+  h.ldx = ldh;
+  h.w = static_cast<const uint16_t*>(head);
+  h.ldw = ldw;
+  h.B = B;
+  h.V = V;
+  h.D = D;
+  return h;
+}
+
+int head_logits(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head, long long ldw, int B, int V, int D,
+                float* logits, long long ldl, hipStream_t st) {
+  if (!ctx) return set_error("vsmp: null context");
+  if (!logits) return set_error("vsmp: logits is required");
+  if (check_head(hidden, ldh, head, ldw, B, V, D, logits, ldl, false) != 0) return -1;
+  HeadArgs h = head_args(hidden, ldh, head, ldw, B, V, D);
+  h.col0 = 0;
+  h.col1 = V;
+  h.out = logits;
+  h.ldo = ldl;
+  launch_head_gemm(h, head_tile(B, false), st);
+  return hip_ok(hipGetLastError(), "head launch") ? 0 : -1;
+}
+
+int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head, long long ldw, int B, int V, int D,
+              const vsmp_params* params, int params_per_row, const int* hist, const int* hist_off, int u_mode,
+              const double* u, unsigned long long* rng_state, unsigned long long counter, int* out, float* logits,
+              long long ldl, const vsmp_debug* dbg, hipStream_t st) {
+  if (!ctx) return set_error("vsmp: null context");
+  if (check_head(hidden, ldh, head, ldw, B, V, D, logits, ldl, true) != 0) return -1;
+  if (!out || !params) return set_error("vsmp: params and out are required");
+  if ((hist == nullptr) != (hist_off == nullptr)) return set_error("vsmp: hist and hist_off go together");
+  if (u_mode == VSMP_U_SUPPLIED && !u) return set_error("vsmp: u is required with VSMP_U_SUPPLIED");
+  if (u_mode == VSMP_U_XORSHIFT && !rng_state) return set_error("vsmp: rng_state is required with VSMP_U_XORSHIFT");
+  if (u_mode < VSMP_U_SUPPLIED || u_mode > VSMP_U_XORSHIFT) return set_error("vsmp: unknown u_mode");
+  const int cand_cap = dbg ? dbg->cand_cap : 0;
+  if (cand_cap < 0 || (cand_cap > 0 && !dbg->cand_ids)) return set_error("vsmp: cand_ids is required with cand_cap > 0");
+  if (cand_cap > kGenCap) return set_error("vsmp: cand_cap is at most " + std::to_string(kGenCap));
+
+  hipEvent_t busy = ctx->done_ev;
+  const bool shared_general = !params_per_row && path_host(*params, V, true) == kPathGeneral;
+  // logits written whole: the caller's, or (general rows possible, none kept by the caller) scratch
+  float* full = logits;
+  long long fld = ldl;
+  if (!full && (shared_general || params_per_row)) {
+    fld = (static_cast<long long>(V) + 3) & ~3LL;
+    if (!grow(ctx->h_full, ctx->n_full, static_cast<size_t>(B) * static_cast<size_t>(fld), false, "head scratch", busy))
+      return -1;
+    full = ctx->h_full;
+  }
+  HeadArgs h = head_args(hidden, ldh, head, ldw, B, V, D);
+  if (shared_general) {  // every row samples the whole row: the head, then the batched pick
+    h.col0 = 0;
+    h.col1 = V;
+    h.out = full;
+    h.ldo = fld;
+    launch_head_gemm(h, head_tile(B, false), st);
+    if (!hip_ok(hipGetLastError(), "head launch")) return -1;
+    return launch_batch(ctx, full, B, V, fld, params, 0, hist, hist_off, u_mode, u, rng_state, counter, out, dbg, st,
+                        nullptr);
+  }
+  const int n0 = std::min(kHeadProbe, V);
+  if (!grow(ctx->h_tk, ctx->n_tk, static_cast<size_t>(B), false, "head scratch", busy) ||
+      !grow(ctx->h_rmode, ctx->n_rmode, static_cast<size_t>(B), false, "head scratch", busy) ||
+      !grow(ctx->h_cnt, ctx->n_hcnt, static_cast<size_t>(B), false, "head scratch", busy) ||
+      !grow(ctx->h_cand, ctx->n_hcand, static_cast<size_t>(B) * static_cast<size_t>(V), false, "head scratch", busy) ||
+      (!full && !grow(ctx->h_probe, ctx->n_probe, static_cast<size_t>(B) * static_cast<size_t>(n0), false, "head scratch", busy)))
+    return -1;
+  float* probe = full ? full : ctx->h_probe;
+  const long long pld = full ? fld : n0;
+  KArgs a = batch_args(full, B, V, full ? fld : V, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
+                       out, dbg);
+  a.S = 1;
+  a.L = V;
+  a.xcd_map = 0;
+  a.smallk_ok = 1;
+  a.gen_fused = 1;
+  if (a.pen_bits) {
+    launch_zero_u32(a.pen_bits, static_cast<long long>(B) * a.words, st);
+    if (!hip_ok(hipGetLastError(), "zero-fill launch")) return -1;
+  }
+  // 1. the probe columns of every row, written
+  HeadArgs hp = h;
+  hp.col0 = 0;
+  hp.col1 = n0;
+  hp.out = probe;
+  hp.ldo = pld;
+  launch_head_gemm(hp, head_tile(B, true), st);
+  if (!hip_ok(hipGetLastError(), "probe launch")) return -1;
+  // 2. per row: the bound, the mode and the probe's candidates
+  h.tk = ctx->h_tk;
+  h.rmode = ctx->h_rmode;
+  h.cand = ctx->h_cand;
+  h.cnt = ctx->h_cnt;
+  h.cap = V;
+  launch_head_bound(a, h, probe, pld, n0, logits != nullptr ? 1 : 0, ctx->h_rmode, ctx->h_tk, st);
+  if (!hip_ok(hipGetLastError(), "bound launch")) return -1;
+  // 3. the other columns: candidates kept, logits written where the row's mode asks
+  if (n0 < V) {
+    HeadArgs hm = h;
+    hm.col0 = n0;
+    hm.col1 = V;
+    hm.out = full;
+    hm.ldo = fld;
+    launch_head_gemm(hm, head_tile(B, false), st);
+    if (!hip_ok(hipGetLastError(), "head launch")) return -1;
+  }
+  // 4. greedy and small-k rows: the exact top-k and the epilogue
+  launch_head_finish(a, h, st);
+  if (!hip_ok(hipGetLastError(), "finish launch")) return -1;
+  // 5. general rows (per-row parameters): the general path over their written logits
+  if (params_per_row) {
+    if (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch", busy) ||
+        !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch", busy) ||
+        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(exact_slots(a.x_n)) * 2 * a.x_n, false, "scratch", busy))
+      return -1;
+    a.x_flag = ctx->x_flag;
+    a.x_u = ctx->x_u;
+    a.x_buf = ctx->x_buf;
+    launch_general(a, st);
+    if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
+    launch_general_exact(a, exact_slots(a.x_n), st);
+    if (!hip_ok(hipGetLastError(), "exact general-path launch")) return -1;
+  }
+  return 0;
+}
+
 // vsmp_pick_batch_noalloc: row mode, one stream, the scratch in the static device array.
 int pick_batch_noalloc(const float* logits, int B, int V, long long ld, const vsmp_params* params, int params_per_row,
                        const int* hist, const int* hist_off, int u_mode, const double* u,
@@ -554,8 +718,10 @@ void vsmp_ctx_free(vsmp_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
-  void* bufs[] = {c->x_flag, c->x_u, c->x_buf, c->s_cand, c->s_cnt, c->s_npen, c->s_max, c->s_min, c->s_bits, c->g_slot, c->g_tick,
-                  c->g_npen, c->d_logits, c->d_hist, c->d_hoff, c->d_u, c->d_out, c->d_info};
+  void* bufs[] = {c->x_flag, c->x_u,    c->x_buf,    c->s_cand, c->s_cnt,   c->s_npen,   c->s_max,
+                  c->s_min,  c->s_bits, c->g_slot,   c->g_tick, c->g_npen,  c->h_probe,  c->h_full,
+                  c->h_tk,   c->h_rmode, c->h_cnt,   c->h_cand, c->d_logits, c->d_hist,  c->d_hoff,
+                  c->d_u,    c->d_out,  c->d_info};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -583,6 +749,26 @@ int vsmp_pick_batch_noalloc(const float* logits, int B, int V, long long ld, con
   vsmp::clear_error();
   return vsmp::pick_batch_noalloc(logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
                                   out, dbg, static_cast<hipStream_t>(stream));
+}
+
+int vsmp_head_logits(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head, long long ldw, int B, int V,
+                     int D, float* logits, long long ldl, void* stream) {
+  vsmp::clear_error();
+  if (ctx && !vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  return vsmp::head_logits(ctx, hidden, ldh, head, ldw, B, V, D, logits, ldl, static_cast<hipStream_t>(stream));
+}
+
+int vsmp_head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head, long long ldw, int B, int V, int D,
+                   const vsmp_params* params, int params_per_row, const int* hist, const int* hist_off, int u_mode,
+                   const double* u, unsigned long long* rng_state, unsigned long long counter, int* out, float* logits,
+                   long long ldl, const vsmp_debug* dbg, void* stream) {
+  vsmp::clear_error();
+  if (ctx && !vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int rc = vsmp::head_pick(ctx, hidden, ldh, head, ldw, B, V, D, params, params_per_row, hist, hist_off, u_mode, u,
+                                 rng_state, counter, out, logits, ldl, dbg, st);
+  if (ctx && !vsmp::mark_done(ctx, st)) return -1;
+  return rc;
 }
 
 int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params* params, const int* hist, int H,

@@ -108,6 +108,48 @@ void launch_topk_split(const KArgs& a, hipStream_t st);
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st);
 void launch_zero_u32(uint32_t* p, long long n, hipStream_t st);
 
+// ---- the LM head and its hand-off to the sampler -------------------------------------------------
+// logits[r][c] = sum_d x[r][d] * w[c][d]: bf16 operands, fp32 accumulation in MFMA order (the same
+// order in every launch and tile shape, so a logit does not depend on how it was computed).
+constexpr int kHeadKC = 64;            // hidden elements per chunk of the product (D % 64 == 0)
+constexpr int kHeadMaxD = 16384;       // largest hidden size accepted
+constexpr int kHeadProbe = 4096;       // columns of the probe product that sets each row's bound
+constexpr int kHeadMaxVocab = 1 << 19; // the finish keeps the row's history bitmap in LDS
+constexpr int kHeadRound = 4096 - 256; // candidates the finish takes per round (its LDS list)
+
+struct HeadArgs {
+  const uint16_t* x;  // bf16 bits [B][ldx]: the hidden states the head multiplies
+  long long ldx;
+  const uint16_t* w;  // bf16 bits [V][ldw]: the head, one row per vocabulary entry
+  long long ldw;
+  int B, V, D;
+  int col0, col1;     // columns [col0, col1) of this launch
+  float* out;         // logits [B][ldo] (column c at out[r * ldo + c - out_col0]) or null
+  long long ldo;
+  int out_col0;
+  // per row: bit 0 keeps the candidates (raw logits whose order key is >= tk[r]) in cand, bit 1
+  // writes the logits to out; null: every row written, nothing kept
+  const uint8_t* rmode;
+  const uint32_t* tk;
+  unsigned long long* cand;  // [B][cap] composites (order key of the raw logit << 32 | ~column)
+  int* cnt;                  // [B] entries in cand
+  long long cap;
+};
+
+// Main-product tile shape for a batch of B rows (index into the kernel instances), and the narrow
+// shape of the probe product.
+int head_tile(int B, bool probe);
+int head_tile_cols(int tile);
+int head_tile_rows(int tile);
+void launch_head_gemm(const HeadArgs& h, int tile, hipStream_t st);
+// Per row, after the probe product: the bound tk (from the probe's penalised logits, src/sampler.cpp
+// semantics), the row's mode and its first candidates (those of the probe columns).
+void launch_head_bound(const KArgs& a, const HeadArgs& h, const float* probe, long long pld, int n0, int write_all,
+                       uint8_t* rmode, uint32_t* tk, hipStream_t st);
+// Per greedy / small-k row, after the main product: the penalty on the candidates, the exact top-k
+// and the reference epilogue (out, info, candidates as vsmp_pick_batch writes them).
+void launch_head_finish(const KArgs& a, const HeadArgs& h, hipStream_t st);
+
 // Sampler::accept (reference src/sampler.cpp:43-48) on device-resident histories: row r's history is
 // hist[off[r], off[r] + len[r]) in a region of `cap` ids. For each of the n rows that is active
 // (active null: every row), the id ids[r] (ids null: `tok`) is appended; with repeat_last > 0 a

@@ -35,6 +35,7 @@
 #include <type_traits>
 
 #include "vsmp_common.hpp"
+#include "vsmp_keys.hpp"
 
 namespace vsmp {
 namespace {
@@ -60,23 +61,6 @@ __device__ __forceinline__ uint4 stream_ld(const void* p) {
   const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
-
-// ---- keys ---------------------------------------------------------------------------------------
-
-__device__ __forceinline__ uint32_t ord_key(float v) {
-  uint32_t b = __float_as_uint(v);
-  if (b == 0x80000000u) b = 0u;  // -0 sorts with +0 (they compare equal in the reference)
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-__device__ __forceinline__ float key_val(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
-__device__ __forceinline__ uint64_t comp(uint32_t key, uint32_t idx) {
-  return (static_cast<uint64_t>(key) << 32) | static_cast<uint32_t>(~idx);
-}
-__device__ __forceinline__ uint32_t comp_key(uint64_t c) { return static_cast<uint32_t>(c >> 32); }
-__device__ __forceinline__ int comp_idx(uint64_t c) { return static_cast<int>(~static_cast<uint32_t>(c)); }
-__device__ __forceinline__ float comp_val(uint64_t c) { return key_val(comp_key(c)); }
 
 // src/sampler.cpp:63, fp32 IEEE division / multiplication
 __device__ __forceinline__ float penalise(float v, float r) { return v > 0.0f ? v / r : v * r; }
@@ -3525,6 +3509,318 @@ __global__ __launch_bounds__(256) void k_numer_probe(const float* __restrict__ d
     y[i] = numer_tab(g, etab, wq, d[i], max(q_of_d(g, d[i]), 0));  // d > 0 (no row holds one) kept in range
 }
 
+// ---- the LM head's hand-off: bound and finish around k_head_gemm -------------------------------
+//
+// The head's product (k_head_gemm, vsmp_head.hip) first computes the probe columns [0, n0) of every
+// row. k_head_bound takes, per greedy / small-k row, the k-th largest penalised logit among them (k
+// = 1 for greedy rows): no element below it can be in the row's top k, since the probe alone holds
+// k elements at or above it. The main product then keeps only the columns whose raw logit reaches
+// the bound (lowered, for repeat < 1, to what a raised history logit would need), and k_head_finish
+// penalises those candidates, takes the exact top-k and runs the reference epilogue. The logits of
+// such rows are never written unless the caller asks for them.
+
+constexpr int kHbNT = 256;
+constexpr int kHbPer = kHeadProbe / kHbNT;  // probe logits per thread
+constexpr int kHfNT = 256;
+constexpr int kHfSmall = 2 * kHfNT;         // lists the finish ranks by counting
+static_assert(kHeadRound + kKmax <= kMergeCap && kEpiWs + kKmax <= kHeadRound + kKmax, "finish buffer");
+
+// The bin (of 2048, counts in hist) that holds the k-th largest entry, bins counted from the top
+// down, and the number of entries in the bins above it: *bin, *above (block-wide, NT threads;
+// *bin = -1 when the bins hold fewer than k entries).
+template <int NT>
+__device__ void bin_of_kth(const uint32_t* hist, uint32_t k, uint32_t* wsum, int* bin, uint32_t* above) {
+  constexpr int per = 2048 / NT;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int top = 2047 - per * tid;  // this thread's bins: top, top - 1, ..., top - per + 1
+  uint32_t c[per];
+  uint32_t s = 0;
+#pragma unroll
+  for (int q = 0; q < per; ++q) {
+    c[q] = hist[top - q];
+    s += c[q];
+  }
+  const uint32_t incl = wave_incl_scan(s);
+  if (tid == 0) *bin = -1;
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  uint32_t before = incl - s;
+  for (int i = 0; i < w; ++i) before += wsum[i];
+  if (before < k && before + s >= k) {
+#pragma unroll
+    for (int q = 0; q < per; ++q) {
+      if (before + c[q] >= k) {
+        *bin = top - q;
+        *above = before;
+        break;
+      }
+      before += c[q];
+    }
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kHbNT) void k_head_bound(KArgs a, HeadArgs h, const float* __restrict__ probe, long long pld,
+                                                      int n0, int write_all, uint8_t* __restrict__ rmode,
+                                                      uint32_t* __restrict__ tk) {
+  __shared__ uint32_t bits[kHeadProbe / 32];
+  __shared__ uint32_t hist[2048];
+  __shared__ uint32_t wsum[kHbNT / 64];
+  __shared__ int sbin;
+  __shared__ uint32_t sabove;
+  __shared__ int scnt;
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const vsmp_params P = row_params(a, row);
+  const int V = a.V;
+  const int path = path_of(P, V, 1);
+  if (path == kPathGeneral) {  // written whole, sampled by k_general
+    if (tid == 0) {
+      rmode[row] = 2;
+      tk[row] = 0xFFFFFFFFu;
+      h.cnt[row] = 0;
+    }
+    return;
+  }
+  // -- history bitmap of the probe columns (src/sampler.cpp:53-65)
+  int h0 = 0, h1 = 0;
+  if (a.hist_off) {
+    h0 = a.hist_off[row];
+    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
+  }
+  const int H = h1 - h0;
+  const bool pen = (P.repeat != 1.0f) && H > 0;
+  const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
+  for (int i = tid; i < kHeadProbe / 32; i += kHbNT) bits[i] = 0u;
+  for (int i = tid; i < 2048; i += kHbNT) hist[i] = 0u;
+  if (tid == 0) scnt = 0;
+  __syncthreads();
+  if (pen) {
+    for (int i = hfrom + tid; i < h1; i += kHbNT) {
+      const int id = a.hist[i];
+      if (id >= 0 && id < n0) atomicOr(&bits[id >> 5], 1u << (id & 31));
+    }
+  }
+  __syncthreads();
+  // -- the probe's logits: raw (for the candidates) and penalised order keys (for the bound)
+  const float* rp = probe + static_cast<long long>(row) * pld;
+  float raw[kHbPer];
+  uint32_t key[kHbPer];
+#pragma unroll
+  for (int j = 0; j < kHbPer; ++j) {
+    const int e = tid + j * kHbNT;
+    raw[j] = e < n0 ? rp[e] : 0.0f;
+    const bool hb = pen && e < n0 && ((bits[e >> 5] >> (e & 31)) & 1u);
+    key[j] = e < n0 ? ord_key(hb ? penalise(raw[j], P.repeat) : raw[j]) : 0u;
+  }
+  const int k = path == kPathGreedy ? 1 : top_k_of(P, V);  // <= n0
+  // -- the k-th largest key, to 22 bits (two 11-bit levels); its lower edge bounds the row's k-th
+#pragma unroll
+  for (int j = 0; j < kHbPer; ++j)
+    if (tid + j * kHbNT < n0) atomicAdd(&hist[key[j] >> 21], 1u);
+  __syncthreads();
+  bin_of_kth<kHbNT>(hist, static_cast<uint32_t>(k), wsum, &sbin, &sabove);
+  const int b1 = sbin;
+  const uint32_t k2 = static_cast<uint32_t>(k) - sabove;
+  for (int i = tid; i < 2048; i += kHbNT) hist[i] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kHbPer; ++j)
+    if (tid + j * kHbNT < n0 && static_cast<int>(key[j] >> 21) == b1) atomicAdd(&hist[(key[j] >> 10) & 2047u], 1u);
+  __syncthreads();
+  bin_of_kth<kHbNT>(hist, k2, wsum, &sbin, &sabove);
+  const uint32_t T = (static_cast<uint32_t>(b1) << 21) | (static_cast<uint32_t>(sbin) << 10);
+  // the raw logit a candidate needs: T itself when the penalty can only lower a logit (repeat >= 1);
+  // for repeat < 1 a history logit rises (v / r for v > 0, v * r otherwise), so the bound is lowered
+  // to the raw value that could reach T, with eight ulps to spare for the rounding of v / r and v * r
+  uint32_t tlo = T;
+  if (pen && P.repeat < 1.0f) {
+    const float t = key_val(T);
+    const float tl = t > 0.0f ? t * P.repeat : (t < 0.0f ? t / P.repeat : t);
+    const uint32_t kl = ord_key(tl);
+    tlo = min(T, kl > 8u ? kl - 8u : 0u);
+  }
+  // -- the probe's candidates
+#pragma unroll
+  for (int j = 0; j < kHbPer; ++j) {
+    const int e = tid + j * kHbNT;
+    const uint32_t rk = ord_key(raw[j]);
+    const bool pass = e < n0 && rk >= tlo;
+    const uint64_t m = __ballot(pass);
+    if (m) {
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&scnt, __popcll(m));
+      base = __shfl(base, 0);
+      if (pass) {
+        const long long pos = base + __popcll(m & ((1ull << lane) - 1ull));
+        h.cand[static_cast<long long>(row) * h.cap + pos] = comp(rk, static_cast<uint32_t>(e));
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    h.cnt[row] = scnt;
+    tk[row] = tlo;
+    rmode[row] = static_cast<uint8_t>(1u | (write_all ? 2u : 0u));
+  }
+}
+
+// A candidate's composite after the row's penalty (the candidates hold raw logits).
+__device__ __forceinline__ uint64_t head_pen(uint64_t c, bool pen, const uint32_t* bits, float rep) {
+  const int e = comp_idx(c);
+  if (!pen || !((bits[e >> 5] >> (e & 31)) & 1u)) return c;
+  return comp(ord_key(penalise(comp_val(c), rep)), static_cast<uint32_t>(e));
+}
+
+// The sorted top-kk of the m distinct composites in buf (m <= kHeadRound + kKmax) into top. Short
+// lists are ranked by counting; longer ones first cut to the entries at or above the bin of the
+// kk-th key in a 2048-bin histogram of the list's key range (ranked by counting when that leaves at
+// most kHfSmall), else sorted whole. buf is clobbered.
+__device__ void head_select(uint64_t* buf, int m, int kk, uint64_t* top, uint64_t* sub, uint32_t* hist,
+                            uint64_t* red64, uint32_t* wsum, int* sint) {
+  const int tid = threadIdx.x;
+  if (m > kHfSmall) {
+    uint64_t lo = ~0ull, hi = 0ull;
+    for (int i = tid; i < m; i += kHfNT) {
+      lo = min64(lo, buf[i]);
+      hi = max64(hi, buf[i]);
+    }
+    const uint32_t kmin = comp_key(block_min64<kHfNT>(lo, red64));
+    const uint32_t kmax = comp_key(block_max64<kHfNT>(hi, red64));
+    const uint32_t span = kmax - kmin;
+    const int nb = 32 - __clz(static_cast<int>(span));  // bit length of the span
+    const int sh = nb > 11 ? nb - 11 : 0;                // (span >> sh) < 2048
+    for (int i = tid; i < 2048; i += kHfNT) hist[i] = 0u;
+    __syncthreads();
+    for (int i = tid; i < m; i += kHfNT) atomicAdd(&hist[(comp_key(buf[i]) - kmin) >> sh], 1u);
+    __syncthreads();
+    bin_of_kth<kHfNT>(hist, static_cast<uint32_t>(kk), wsum, &sint[0], reinterpret_cast<uint32_t*>(&sint[1]));
+    const int b = sint[0];
+    const int keep = b < 0 ? m : static_cast<int>(static_cast<uint32_t>(sint[1]) + hist[b]);
+    if (keep <= kHfSmall) {
+      if (tid == 0) sint[2] = 0;
+      __syncthreads();
+      for (int i = tid; i < m; i += kHfNT) {
+        const uint64_t x = buf[i];
+        if (static_cast<int>((comp_key(x) - kmin) >> sh) >= b) sub[atomicAdd(&sint[2], 1)] = x;
+      }
+      __syncthreads();
+      select_top<kHfNT>(sub, keep, kk, top);
+      return;
+    }
+  }
+  select_top<kHfNT>(buf, m, kk, top);
+}
+
+__global__ __launch_bounds__(kHfNT) void k_head_finish(KArgs a, HeadArgs h) {
+  __shared__ __align__(16) uint64_t buf[kHeadRound + kKmax];
+  __shared__ __align__(16) uint64_t sub[kHfSmall + 16];
+  __shared__ uint64_t top[kKmax];
+  __shared__ uint32_t hist[2048];
+  __shared__ uint64_t red64[kHfNT / 64];
+  __shared__ uint32_t red32[kHfNT / 64];
+  __shared__ int sint[4];
+  extern __shared__ uint32_t bits[];  // the row's history bitmap, ceil(V/32) words
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const vsmp_params P = row_params(a, row);
+  const int V = a.V;
+  const int path = path_of(P, V, 1);
+  if (path == kPathGeneral) return;
+  int h0 = 0, h1 = 0;
+  if (a.hist_off) {
+    h0 = a.hist_off[row];
+    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
+  }
+  const int H = h1 - h0;
+  const bool pen = (P.repeat != 1.0f) && H > 0;
+  const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
+  const int words = (V + 31) >> 5;
+  uint32_t np = 0;
+  if (pen) {  // src/sampler.cpp:53-65
+    for (int i = tid; i < words; i += kHfNT) bits[i] = 0u;
+    __syncthreads();
+    for (int i = hfrom + tid; i < h1; i += kHfNT) {
+      const int id = a.hist[i];
+      if (id >= 0 && id < V) atomicOr(&bits[id >> 5], 1u << (id & 31));
+    }
+    __syncthreads();
+    for (int i = tid; i < words; i += kHfNT) np += __popc(bits[i]);
+    if (a.pen_bits) store_pen_words<kHfNT>(a, row, 0, bits, words);
+  }
+  const int n_pen = static_cast<int>(block_sum_u32<kHfNT>(np, red32));
+  const long long cap = h.cap;
+  const int n = static_cast<int>(min(static_cast<long long>(h.cnt[row]), cap));
+  const uint64_t* list = reinterpret_cast<const uint64_t*>(h.cand) + static_cast<long long>(row) * cap;
+
+  if (path == kPathGreedy) {  // src/sampler.cpp:66-70: the first maximum
+    uint64_t b = 0ull;
+    for (int i = tid; i < n; i += kHfNT) b = max64(b, head_pen(list[i], pen, bits, P.repeat));
+    b = block_max64<kHfNT>(b, red64);
+    if (tid == 0) {
+      const int id = comp_idx(b);
+      a.out[row] = id;
+      if (a.info) {
+        vsmp_row_info inf = {};
+        inf.id = id;
+        inf.path = kPathGreedy;
+        inf.k = inf.keep_minp = inf.keep = 1;
+        inf.rank = 0;
+        inf.last_id = id;
+        inf.mx = comp_val(b);
+        inf.n_pen = n_pen;
+        a.info[row] = inf;
+      }
+    }
+    return;
+  }
+
+  // -- the exact top-k, in rounds of kHeadRound candidates: each round adds the candidates above the
+  // k-th composite so far to the k kept from the rounds before
+  const int k = top_k_of(P, V);
+  int have = 0;
+  uint64_t bound = 0ull;
+  int kk = 0;
+  for (int base = 0; base < n; base += kHeadRound) {
+    const int mr = min(kHeadRound, n - base);
+    if (tid == 0) sint[3] = 0;
+    __syncthreads();
+    for (int i = tid; i < mr; i += kHfNT) {
+      const uint64_t c = head_pen(list[base + i], pen, bits, P.repeat);
+      if (c > bound) buf[have + atomicAdd(&sint[3], 1)] = c;
+    }
+    __syncthreads();
+    const int m = have + sint[3];
+    const bool last = base + kHeadRound >= n;
+    __syncthreads();
+    if (m > k || last) {
+      kk = min(k, m);
+      head_select(buf, m, kk, top, sub, hist, red64, red32, sint);
+      __syncthreads();
+      if (!last) {
+        for (int i = tid; i < kk; i += kHfNT) buf[i] = top[i];
+        have = kk;
+        bound = kk == k ? top[k - 1] : 0ull;
+        __syncthreads();
+      }
+    } else {
+      have = m;
+    }
+  }
+  __syncthreads();
+  // -- src/sampler.cpp:79-108 on the sorted top-k (kk == k: the probe alone holds k candidates)
+  if (tid < 64) {
+    double u = 0.0;
+    if (tid == 0) u = draw_u(a, row, P);
+    double* spr = reinterpret_cast<double*>(buf) + kEpiWs;
+    const float mx = comp_val(top[0]);
+    for (int i = tid; i < kk; i += 64) spr[i] = numer(comp_val(top[i]), mx, P.temp);
+    wave_lds_sync();
+    if (kk <= 64)
+      epilogue_wave<1>(a, row, P, top, spr, kk, n_pen, 0, readlane_f64(u, 0), reinterpret_cast<double*>(buf));
+    else
+      epilogue_wave<kEpiJ>(a, row, P, top, spr, kk, n_pen, 0, readlane_f64(u, 0), reinterpret_cast<double*>(buf));
+  }
+}
+
 }  // namespace
 
 void launch_numer_probe(const float* d, double* y, long long n, float temp, float qs, hipStream_t st) {
@@ -3573,6 +3869,22 @@ void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st) {
       hipLaunchKernelGGL(k_stage1<64>, dim3(grid), dim3(kTpb), 0, st, a);
       break;
   }
+}
+
+void launch_head_bound(const KArgs& a, const HeadArgs& h, const float* probe, long long pld, int n0, int write_all,
+                       uint8_t* rmode, uint32_t* tk, hipStream_t st) {
+  hipLaunchKernelGGL(k_head_bound, dim3(a.B), dim3(kHbNT), 0, st, a, h, probe, pld, n0, write_all, rmode, tk);
+}
+
+void launch_head_finish(const KArgs& a, const HeadArgs& h, hipStream_t st) {
+  const size_t dyn = static_cast<size_t>((a.V + 31) / 32) * sizeof(uint32_t);
+  static bool configured = false;
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_head_finish), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(kRowMaxDynLds));
+    configured = true;
+  }
+  hipLaunchKernelGGL(k_head_finish, dim3(a.B), dim3(kHfNT), dyn, st, a, h);
 }
 
 void launch_finish(const KArgs& a, hipStream_t st) {
