@@ -37,6 +37,9 @@ DESCR = {
     "wide": "wide: 512 x 151936 fp32 N(0,0.5^2), top-k 0, top-p .99, temp 1, no penalty",
     "mixed": ("mixed: 1024 x 128256 fp32 N(0,2^2)+spikes, per-row temp/top-k/top-p/min-p/repeat, H U[0,2048], "
               "25% greedy"),
+    "head": ("head: LM head 256 x 896 bf16 hidden states against a 151936 x 896 bf16 head (Qwen2.5-0.5B's "
+             "shape), fp32 logits, then the peaked workload's sampler (temp .8, top-k 50, top-p .95, min-p .05, "
+             "repeat 1.1 over H=512), counter-RNG draws"),
 }
 
 
@@ -193,6 +196,93 @@ def bench_single(args):
     }
 
 
+def bench_head(args):
+    """The LM head with the sampler fused into it (vsmp_head_pick) against the same work unfused (the
+    head's logits written by vsmp_head_logits, then vsmp_pick_batch over them), and the head's
+    product alone. Each variant: K steps captured into a HIP graph and replayed, timed by two events
+    on the launch stream; the head rotates over three copies (816 MB) so that no step finds it in
+    the 256 MB Infinity Cache. value = rows/s of the fused call."""
+    import numpy as np
+    import torch
+
+    import verbo_amd as V
+
+    B, Vv, D, H = 256, 151936, 896, 512
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    hidden = torch.randn(B, D, device=dev, generator=g).to(torch.bfloat16)
+    heads = [(torch.randn(Vv, D, device=dev, generator=g) * (3.0 / D ** 0.5)).to(torch.bfloat16) for _ in range(3)]
+    rng = np.random.default_rng(7)
+    hist = torch.from_numpy(rng.integers(0, Vv, B * H).astype(np.int32)).to(dev)
+    hoff = torch.from_numpy(np.arange(0, B * H + 1, H, dtype=np.int32)).to(dev)
+    prm = V.Params(temp=0.8, top_k=50, top_p=0.95, min_p=0.05, repeat=1.1, repeat_last=0, seed=0)
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    lg = torch.empty(B, Vv, dtype=torch.float32, device=dev)
+    ctx = V.Context(0)
+    stream = torch.cuda.current_stream(dev)
+
+    def fused(i, st):
+        ctx.head_pick(hidden, heads[i % 3], prm, hist, hoff, V.U_COUNTER, counter=i, out=out, stream=st)
+
+    def unfused(i, st):
+        ctx.head_logits(hidden, heads[i % 3], logits=lg, stream=st)
+        ctx.pick_batch(lg, prm, hist, hoff, V.U_COUNTER, counter=i, out=out, stream=st)
+
+    def product(i, st):
+        ctx.head_logits(hidden, heads[i % 3], logits=lg, stream=st)
+
+    def timed(fn):
+        for i in range(args.warmup):
+            fn(i, stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream(dev)
+        cap.wait_stream(stream)
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(args.steps):
+                fn(args.warmup + i, cap)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    ms = {name: timed(fn) for name, fn in (("fused", fused), ("unfused", unfused), ("product", product))}
+    for k_, v in ms.items():
+        log(f"[bench] head: {k_} {v * 1e3:.1f} us/step")
+    head_bytes = Vv * D * 2
+    alg = head_bytes + B * D * 2 + B * 64 * 4 + B * 4  # head, hidden, the penalised ids read, ids out
+    achieved = alg / (ms["fused"] * 1e-3) / 1e9
+    flops = 2.0 * B * Vv * D
+    return {
+        "metric": f"sampled rows/s, {DESCR['head']}",
+        "value": B / (ms["fused"] * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms["fused"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": DESCR["head"], "B": B, "V": Vv, "D": D, "head_copies": 3,
+                   "algorithmic_bytes_per_step": alg, "issue": "hip_graph",
+                   "unfused_ms_per_step": ms["unfused"], "product_ms_per_step": ms["product"],
+                   "mfma_tflops_fused": flops / (ms["fused"] * 1e-3) / 1e12,
+                   "mfma_tflops_product": flops / (ms["product"] * 1e-3) / 1e12},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "cpu_baseline": None,
+    }
+
+
 def traffic_from_profiles(name):
     """HBM bytes per call measured by rocprofv3 PMC runs (profiles/<workload>_traffic.json)."""
     p = ROOT / "profiles" / f"{name}_traffic.json"
@@ -232,6 +322,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a ROCm device"
     if args.workload == "single":
         print(json.dumps(bench_single(args)), flush=True)
+        return
+    if args.workload == "head":
+        print(json.dumps(bench_head(args)), flush=True)
         return
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()

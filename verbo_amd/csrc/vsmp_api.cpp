@@ -120,10 +120,10 @@ struct vsmp_ctx {
   size_t n_tk = 0;
   unsigned char* h_rmode = nullptr;
   size_t n_rmode = 0;
-  int* h_cnt = nullptr;
-  size_t n_hcnt = 0;
-  unsigned long long* h_cand = nullptr;
-  size_t n_hcand = 0;
+  unsigned long long* h_rcand = nullptr;  // candidates, one list per row
+  size_t n_rcand = 0;
+  int* h_rcnt = nullptr;
+  size_t n_rcnt = 0;
   // host-pointer path buffers
   float* d_logits = nullptr;
   size_t n_logits = 0;
@@ -491,8 +491,8 @@ int check_head(const void* hidden, long long ldh, const void* head, long long ld
   if (D < kHeadKC || D % kHeadKC != 0 || D > kHeadMaxD)
     return set_error("vsmp: D must be a multiple of " + std::to_string(kHeadKC) + " in [" + std::to_string(kHeadKC) + ", " +
                      std::to_string(kHeadMaxD) + "]");
-  if (ldh < D || ldw < D || ldh % 8 != 0 || ldw % 8 != 0)
-    return set_error("vsmp: ldh and ldw must be >= D and multiples of 8 (16-byte rows)");
+  if (ldh < D || ldw < D || ldh % 8 != 0 || ldw % 8 != 0 || ldh >= (1LL << 23) || ldw >= (1LL << 23))
+    return set_error("vsmp: ldh and ldw must be >= D, below 2^23 and multiples of 8 (16-byte rows)");
   if (((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(head)) & 15u) != 0)
     return set_error("vsmp: hidden and head must be 16-byte aligned");
   if (logits && ldl < V) return set_error("vsmp: ldl must be >= V");
@@ -565,10 +565,11 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
                         nullptr);
   }
   const int n0 = std::min(kHeadProbe, V);
+  const int tile = head_tile(B, false);
   if (!grow(ctx->h_tk, ctx->n_tk, static_cast<size_t>(B), false, "head scratch", busy) ||
       !grow(ctx->h_rmode, ctx->n_rmode, static_cast<size_t>(B), false, "head scratch", busy) ||
-      !grow(ctx->h_cnt, ctx->n_hcnt, static_cast<size_t>(B), false, "head scratch", busy) ||
-      !grow(ctx->h_cand, ctx->n_hcand, static_cast<size_t>(B) * static_cast<size_t>(V), false, "head scratch", busy) ||
+      !grow(ctx->h_rcand, ctx->n_rcand, static_cast<size_t>(B) * static_cast<size_t>(V), false, "head scratch", busy) ||
+      !grow(ctx->h_rcnt, ctx->n_rcnt, static_cast<size_t>(B), false, "head scratch", busy) ||
       (!full && !grow(ctx->h_probe, ctx->n_probe, static_cast<size_t>(B) * static_cast<size_t>(n0), false, "head scratch", busy)))
     return -1;
   float* probe = full ? full : ctx->h_probe;
@@ -595,9 +596,9 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
   // 2. per row: the bound, the mode and the probe's candidates
   h.tk = ctx->h_tk;
   h.rmode = ctx->h_rmode;
-  h.cand = ctx->h_cand;
-  h.cnt = ctx->h_cnt;
-  h.cap = V;
+  h.rcand = ctx->h_rcand;
+  h.rcnt = ctx->h_rcnt;
+  h.rcap = V;
   launch_head_bound(a, h, probe, pld, n0, logits != nullptr ? 1 : 0, ctx->h_rmode, ctx->h_tk, st);
   if (!hip_ok(hipGetLastError(), "bound launch")) return -1;
   // 3. the other columns: candidates kept, logits written where the row's mode asks
@@ -607,7 +608,7 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
     hm.col1 = V;
     hm.out = full;
     hm.ldo = fld;
-    launch_head_gemm(hm, head_tile(B, false), st);
+    launch_head_gemm(hm, tile, st);
     if (!hip_ok(hipGetLastError(), "head launch")) return -1;
   }
   // 4. greedy and small-k rows: the exact top-k and the epilogue
@@ -720,7 +721,7 @@ void vsmp_ctx_free(vsmp_ctx* c) {
   (void)hipDeviceSynchronize();
   void* bufs[] = {c->x_flag, c->x_u,    c->x_buf,    c->s_cand, c->s_cnt,   c->s_npen,   c->s_max,
                   c->s_min,  c->s_bits, c->g_slot,   c->g_tick, c->g_npen,  c->h_probe,  c->h_full,
-                  c->h_tk,   c->h_rmode, c->h_cnt,   c->h_cand, c->d_logits, c->d_hist,  c->d_hoff,
+                  c->h_tk,   c->h_rmode, c->h_rcand, c->h_rcnt, c->d_logits, c->d_hist, c->d_hoff,
                   c->d_u,    c->d_out,  c->d_info};
   for (void* p : bufs)
     if (p) (void)hipFree(p);

@@ -127,13 +127,16 @@ struct HeadArgs {
   float* out;         // logits [B][ldo] (column c at out[r * ldo + c - out_col0]) or null
   long long ldo;
   int out_col0;
-  // per row: bit 0 keeps the candidates (raw logits whose order key is >= tk[r]) in cand, bit 1
-  // writes the logits to out; null: every row written, nothing kept
+  // per row: bit 0 keeps the candidates (raw logits whose order key is >= tk[r]), bit 1 writes the
+  // logits to out; null: every row written, nothing kept
   const uint8_t* rmode;
   const uint32_t* tk;
-  unsigned long long* cand;  // [B][cap] composites (order key of the raw logit << 32 | ~column)
-  int* cnt;                  // [B] entries in cand
-  long long cap;
+  // candidates, as composites (order key of the raw logit << 32 | ~column), one list per row: row
+  // r's rcnt[r] at rcand[r * rcap ...] (the probe's first, from k_head_bound, which also sets the
+  // count; then each main tile's, appended at a range it reserves)
+  unsigned long long* rcand;
+  int* rcnt;
+  long long rcap;
 };
 
 // Main-product tile shape for a batch of B rows (index into the kernel instances), and the narrow

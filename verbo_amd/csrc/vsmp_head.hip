@@ -13,8 +13,8 @@
 //
 // Epilogue, per element: the logit is written (rows in write mode) and/or kept as a candidate
 // composite when its order key reaches the row's bound (rows in filter mode). Candidates are rare
-// (the bound is the k-th largest logit of the probe columns), so a wave appends them with one
-// device-scope atomic per row half that holds any.
+// (the bound is the k-th largest logit of the probe columns); a tile reserves each row's range in
+// that row's candidate list with one device-scope atomic.
 #include "vsmp_common.hpp"
 #include "vsmp_keys.hpp"
 
@@ -28,40 +28,66 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kHStr = kHeadKC + 8;  // bf16 per LDS row: 144 bytes, so the 16-byte reads of eight
                                     // consecutive rows fall on distinct banks
 
-// One chunk of the product's operands: 16-byte pieces from global memory into registers (the head
-// with the non-temporal hint: it is read once), then into the LDS tiles.
-template <int PX, int PW>
-__device__ __forceinline__ void chunk_load(const uint16_t* const (&xs)[PX], const uint16_t* const (&ws)[PW], int kc,
-                                           u32x4 (&px)[PX], u32x4 (&pw)[PW]) {
+// The 16-byte pieces of one chunk that a thread moves: piece p = tid + q * NT of the x chunk (row
+// p / 8, part p % 8) and of the w chunk. Pieces past the tile's last row or column read that last
+// row or column (their results are dropped); q past the piece count loads nothing.
+template <int QX, int QW, int NT, int NPX, int NPW>
+__device__ __forceinline__ void chunk_load(const uint16_t* xb, const uint16_t* wb, const int (&xo)[QX],
+                                           const int (&wo)[QW], int kc, u32x4 (&px)[QX], u32x4 (&pw)[QW]) {
+  const int tid = threadIdx.x;
 #pragma unroll
-  for (int q = 0; q < PX; ++q) px[q] = *reinterpret_cast<const u32x4*>(xs[q] + kc);
+  for (int q = 0; q < QX; ++q)
+    if (NPX % NT == 0 || tid + q * NT < NPX) px[q] = *reinterpret_cast<const u32x4*>(xb + xo[q] + kc);
 #pragma unroll
-  for (int q = 0; q < PW; ++q) pw[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ws[q] + kc));
+  for (int q = 0; q < QW; ++q)
+    if (NPW % NT == 0 || tid + q * NT < NPW)
+      pw[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + wo[q] + kc));
 }
-template <int PX, int PW>
-__device__ __forceinline__ void chunk_store(uint16_t* sX, uint16_t* sW, int tid, const u32x4 (&px)[PX],
-                                            const u32x4 (&pw)[PW]) {
+template <int QX, int QW, int NT, int NPX, int NPW>
+__device__ __forceinline__ void chunk_store(uint16_t* sX, uint16_t* sW, const u32x4 (&px)[QX], const u32x4 (&pw)[QW]) {
+  const int tid = threadIdx.x;
 #pragma unroll
-  for (int q = 0; q < PX; ++q) {
-    const int p = tid + 256 * q;
-    *reinterpret_cast<u32x4*>(&sX[(p >> 3) * kHStr + 8 * (p & 7)]) = px[q];
+  for (int q = 0; q < QX; ++q) {
+    const int p = tid + q * NT;
+    if (NPX % NT == 0 || p < NPX) *reinterpret_cast<u32x4*>(&sX[(p >> 3) * kHStr + 8 * (p & 7)]) = px[q];
   }
 #pragma unroll
-  for (int q = 0; q < PW; ++q) {
-    const int p = tid + 256 * q;
-    *reinterpret_cast<u32x4*>(&sW[(p >> 3) * kHStr + 8 * (p & 7)]) = pw[q];
+  for (int q = 0; q < QW; ++q) {
+    const int p = tid + q * NT;
+    if (NPW % NT == 0 || p < NPW) *reinterpret_cast<u32x4*>(&sW[(p >> 3) * kHStr + 8 * (p & 7)]) = pw[q];
   }
 }
 
-template <int WMB, int WNB, int WM, int WN>
-__global__ __launch_bounds__(256) void k_head_gemm(HeadArgs h) {
-  static_assert(WM * WN == 4, "four waves");
+// One chunk's products from the LDS stage: four k-steps of 16, WMB x WNB MFMA blocks each.
+template <int WMB, int WNB>
+__device__ __forceinline__ void mma_chunk(const uint16_t* X, const uint16_t* W, int ra, int cb, int ko,
+                                          f32x16 (&acc)[WMB][WNB]) {
+#pragma unroll
+  for (int s = 0; s < kHeadKC / 16; ++s) {
+    bf16x8 a[WMB], b[WNB];
+#pragma unroll
+    for (int i = 0; i < WMB; ++i) a[i] = *reinterpret_cast<const bf16x8*>(&X[(ra + 32 * i) * kHStr + ko + 8 * s]);
+#pragma unroll
+    for (int j = 0; j < WNB; ++j) b[j] = *reinterpret_cast<const bf16x8*>(&W[(cb + 32 * j) * kHStr + ko + 8 * s]);
+#pragma unroll
+    for (int i = 0; i < WMB; ++i)
+#pragma unroll
+      for (int j = 0; j < WNB; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// WMB x WNB blocks of 32 x 32 per wave, WM x WN waves, R chunks in flight per thread (a ring of
+// registers: chunk c is loaded R chunks before it is used, and loads are consumed in the order they
+// were issued, so each wait covers only the oldest chunk), two LDS stages.
+template <int WMB, int WNB, int WM, int WN, int R>
+__global__ __launch_bounds__(64 * WM * WN) void k_head_gemm(HeadArgs h) {
+  constexpr int NT = 64 * WM * WN;
   constexpr int BM = WM * WMB * 32, BN = WN * WNB * 32;
-  constexpr int PX = BM * (kHeadKC / 8) / 256;  // 16-byte pieces of the x chunk per thread
-  constexpr int PW = BN * (kHeadKC / 8) / 256;  // ... of the w chunk
-  static_assert(PX >= 1 && PW >= 1, "whole pieces per thread");
-  __shared__ __align__(16) uint16_t sX[BM * kHStr];
-  __shared__ __align__(16) uint16_t sW[BN * kHStr];
+  constexpr int NPX = BM * (kHeadKC / 8), NPW = BN * (kHeadKC / 8);  // 16-byte pieces per chunk
+  constexpr int QX = (NPX + NT - 1) / NT, QW = (NPW + NT - 1) / NT;
+  static_assert(R % 2 == 0, "the LDS stage of chunk c0 + r is r % 2");
+  __shared__ __align__(16) uint16_t sX[2][BM * kHStr];
+  __shared__ __align__(16) uint16_t sW[2][BN * kHStr];
   __shared__ uint32_t sT[BM];
   __shared__ uint8_t sM[BM];
 
@@ -71,23 +97,21 @@ __global__ __launch_bounds__(256) void k_head_gemm(HeadArgs h) {
   const int n0 = h.col0 + blockIdx.x * BN;
   const int cend = h.col1;
   const int B = h.B;
-
-  // rows past B and columns past cend read the last valid row (their results are dropped)
-  const uint16_t* xs[PX];
-  const uint16_t* ws[PW];
+  const uint16_t* xb = h.x + static_cast<long long>(m0) * h.ldx;
+  const uint16_t* wb = h.w + static_cast<long long>(n0) * h.ldw;
+  int xo[QX], wo[QW];
 #pragma unroll
-  for (int q = 0; q < PX; ++q) {
-    const int p = tid + 256 * q;
-    xs[q] = h.x + static_cast<long long>(min(m0 + (p >> 3), B - 1)) * h.ldx + 8 * (p & 7);
+  for (int q = 0; q < QX; ++q) {
+    const int p = tid + q * NT;
+    xo[q] = min(p >> 3, B - 1 - m0) * static_cast<int>(h.ldx) + 8 * (p & 7);
   }
 #pragma unroll
-  for (int q = 0; q < PW; ++q) {
-    const int p = tid + 256 * q;
-    ws[q] = h.w + static_cast<long long>(min(n0 + (p >> 3), cend - 1)) * h.ldw + 8 * (p & 7);
+  for (int q = 0; q < QW; ++q) {
+    const int p = tid + q * NT;
+    wo[q] = min(p >> 3, cend - 1 - n0) * static_cast<int>(h.ldw) + 8 * (p & 7);
   }
-  u32x4 px[PX], pw[PW];
   if (h.rmode) {
-    for (int i = tid; i < BM; i += 256) {
+    for (int i = tid; i < BM; i += NT) {
       const int r = m0 + i;
       sM[i] = r < B ? h.rmode[r] : 0;
       sT[i] = r < B ? h.tk[r] : 0xFFFFFFFFu;
@@ -105,29 +129,39 @@ __global__ __launch_bounds__(256) void k_head_gemm(HeadArgs h) {
   const int ra = wm * WMB * 32 + (lane & 31);  // the lane's A row in the tile (block 0)
   const int cb = wn * WNB * 32 + (lane & 31);  // the lane's B column in the tile (block 0)
   const int ko = 32 * (lane >> 5);
+  const int nch = h.D / kHeadKC;
 
-  chunk_load<PX, PW>(xs, ws, 0, px, pw);
-  chunk_store<PX, PW>(sX, sW, tid, px, pw);
-  __syncthreads();
-  for (int kc = 0; kc < h.D; kc += kHeadKC) {
-    const bool more = kc + kHeadKC < h.D;
-    if (more) chunk_load<PX, PW>(xs, ws, kc + kHeadKC, px, pw);
+  // the ring: chunk c lives in slot c % R from its load until its LDS store into stage c % 2, which
+  // happens while chunk c - 1 is multiplied from the other stage (the barrier before it makes
+  // stage c % 2 free and chunk c - 1 visible). The steady-state loop always reloads the slot it
+  // stores (past the last chunk, the last chunk again), so that every wait in it is for the oldest
+  // slot only; the last chunks follow without loads.
+  u32x4 rx[R][QX], rw[R][QW];
 #pragma unroll
-    for (int s = 0; s < kHeadKC / 16; ++s) {
-      bf16x8 a[WMB], b[WNB];
+  for (int r = 0; r < R; ++r)
+    chunk_load<QX, QW, NT, NPX, NPW>(xb, wb, xo, wo, min(r, nch - 1) * kHeadKC, rx[r], rw[r]);
+  chunk_store<QX, QW, NT, NPX, NPW>(sX[0], sW[0], rx[0], rw[0]);
+  chunk_load<QX, QW, NT, NPX, NPW>(xb, wb, xo, wo, min(R, nch - 1) * kHeadKC, rx[0], rw[0]);
+  int c0 = 0;
+  for (; c0 + R < nch; c0 += R) {  // chunks c0 .. c0 + R - 1 multiplied, c0 + 1 .. c0 + R stored
 #pragma unroll
-      for (int i = 0; i < WMB; ++i) a[i] = *reinterpret_cast<const bf16x8*>(&sX[(ra + 32 * i) * kHStr + ko + 8 * s]);
-#pragma unroll
-      for (int j = 0; j < WNB; ++j) b[j] = *reinterpret_cast<const bf16x8*>(&sW[(cb + 32 * j) * kHStr + ko + 8 * s]);
-#pragma unroll
-      for (int i = 0; i < WMB; ++i)
-#pragma unroll
-        for (int j = 0; j < WNB; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    for (int r = 0; r < R; ++r) {
+      const int c = c0 + r;
+      __syncthreads();  // stage c % 2 holds chunk c; stage (c + 1) % 2 is no longer read
+      const int rn = (r + 1) % R;
+      chunk_store<QX, QW, NT, NPX, NPW>(sX[(r + 1) & 1], sW[(r + 1) & 1], rx[rn], rw[rn]);
+      chunk_load<QX, QW, NT, NPX, NPW>(xb, wb, xo, wo, min(c + 1 + R, nch - 1) * kHeadKC, rx[rn], rw[rn]);
+      mma_chunk<WMB, WNB>(sX[r & 1], sW[r & 1], ra, cb, ko, acc);
     }
-    __syncthreads();
-    if (more) {
-      chunk_store<PX, PW>(sX, sW, tid, px, pw);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {  // the last chunks (at most R): no loads
+    const int c = c0 + r;
+    if (c < nch) {
       __syncthreads();
+      const int rn = (r + 1) % R;
+      if (c + 1 < nch) chunk_store<QX, QW, NT, NPX, NPW>(sX[(r + 1) & 1], sW[(r + 1) & 1], rx[rn], rw[rn]);
+      mma_chunk<WMB, WNB>(sX[r & 1], sW[r & 1], ra, cb, ko, acc);
     }
   }
 
@@ -147,33 +181,70 @@ __global__ __launch_bounds__(256) void k_head_gemm(HeadArgs h) {
       }
     return;
   }
+  // candidates (rare: the bound is about the k-th largest logit of the probe's columns), appended
+  // to their rows' lists: pass 1 marks each lane's candidates in a bit mask per block and counts
+  // them per row in LDS; one device-scope atomic per row then reserves the tile's range in the
+  // row's list; pass 2 writes each candidate at its row's next slot
+  __syncthreads();                                // every wave is done with the LDS stages
+  int* rc = reinterpret_cast<int*>(&sX[0][0]);    // [BM] candidates per row, then the next slot
+  for (int t = tid; t < BM; t += NT) rc[t] = 0;
+  __syncthreads();
+  const bool wout = h.out != nullptr;
+  uint32_t pb[WMB][WNB];  // bit r: the lane's element of register r is a candidate
+#pragma unroll
+  for (int i = 0; i < WMB; ++i) {
+    uint32_t tr[16];
+    uint32_t fm = 0u, wmk = 0u;  // rows kept (filter mode, < B) / written
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int rt = wm * WMB * 32 + 32 * i + 8 * (r >> 2) + 4 * hl + (r & 3);
+      const uint32_t md = sM[rt];
+      tr[r] = sT[rt];
+      const uint32_t in = (m0 + rt < B) ? 1u : 0u;
+      fm |= (in & md & 1u) << r;
+      wmk |= (in & (md >> 1) & 1u) << r;
+    }
+#pragma unroll
+    for (int j = 0; j < WNB; ++j) {
+      const int col = n0 + wn * WNB * 32 + 32 * j + cl;
+      const uint32_t cok = col < cend ? 0xFFFFu : 0u;
+      if (wout && (wmk & cok)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * WMB * 32 + 32 * i + 8 * (r >> 2) + 4 * hl + (r & 3);
+          if ((wmk & cok) >> r & 1u) h.out[row * h.ldo + (col - h.out_col0)] = acc[i][j][r];
+        }
+      }
+      uint32_t b = 0u;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) b |= static_cast<uint32_t>(ord_key(acc[i][j][r]) >= tr[r]) << r;
+      b &= fm & cok;
+      pb[i][j] = b;
+      for (uint32_t bb = b; bb; bb &= bb - 1u) {
+        const int r = __ffs(static_cast<int>(bb)) - 1;
+        atomicAdd(&rc[wm * WMB * 32 + 32 * i + 8 * (r >> 2) + 4 * hl + (r & 3)], 1);
+      }
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < BM; t += NT) {
+    const int c = rc[t];
+    rc[t] = c ? atomicAdd(&h.rcnt[m0 + t], c) : 0;  // the tile's range in the row's list
+  }
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < WMB; ++i) {
 #pragma unroll
     for (int j = 0; j < WNB; ++j) {
-      const int col = n0 + wn * WNB * 32 + 32 * j + cl;
-      const bool cok = col < cend;
+      const uint32_t col = static_cast<uint32_t>(n0 + wn * WNB * 32 + 32 * j + cl);
+      for (uint32_t bb = pb[i][j]; bb; bb &= bb - 1u) {
+        const int r = __ffs(static_cast<int>(bb)) - 1;
+        const int rt = wm * WMB * 32 + 32 * i + 8 * (r >> 2) + 4 * hl + (r & 3);
+        float v = acc[i][j][0];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rt = wm * WMB * 32 + 32 * i + 8 * (r >> 2) + 4 * hl + (r & 3);  // row in the tile
-        const int row = m0 + rt;
-        const float v = acc[i][j][r];
-        const bool ok = cok && row < B;
-        const uint32_t md = sM[rt];
-        if (h.out && ok && (md & 2u)) h.out[row * h.ldo + (col - h.out_col0)] = v;
-        const uint32_t key = ord_key(v);
-        const bool pass = ok && (md & 1u) && key >= sT[rt];
-        const uint64_t m = __ballot(pass);
-        if (m) {
-          const uint32_t half = hl ? static_cast<uint32_t>(m >> 32) : static_cast<uint32_t>(m);
-          int base = 0;
-          if (cl == 0 && half) base = atomicAdd(&h.cnt[row], __popc(half));
-          base = __shfl(base, lane & 32);
-          if (pass) {
-            const long long pos = base + __popc(half & ((1u << cl) - 1u));
-            if (pos < h.cap) h.cand[row * h.cap + pos] = comp(key, static_cast<uint32_t>(col));
-          }
-        }
+        for (int q = 1; q < 16; ++q) v = r == q ? acc[i][j][q] : v;
+        const int pos = atomicAdd(&rc[rt], 1);
+        if (pos < h.rcap) h.rcand[static_cast<long long>(m0 + rt) * h.rcap + pos] = comp(ord_key(v), col);
       }
     }
   }
@@ -182,16 +253,17 @@ __global__ __launch_bounds__(256) void k_head_gemm(HeadArgs h) {
 struct TileShape {
   int rows, cols;
 };
-// 0..3: main products (B > 128, > 64, > 32, <= 32); 4..6: probe products (narrow columns)
-constexpr TileShape kTiles[] = {{256, 128}, {128, 128}, {64, 128}, {32, 128}, {256, 32}, {128, 32}, {64, 64}};
+// 0..3: main products (B > 128, > 64, > 32, <= 32); 4, 5: probe products (narrow tiles, so that
+// many workgroups share the few probe columns: B > 32, B <= 32)
+constexpr TileShape kTiles[] = {{256, 128}, {128, 128}, {64, 128}, {32, 128}, {64, 32}, {32, 32}};
 
 }  // namespace
 
 int head_tile(int B, bool probe) {
-  if (B > 128) return probe ? 4 : 0;
-  if (B > 64) return probe ? 5 : 1;
-  if (B > 32) return probe ? 6 : 2;
-  return 3;
+  if (probe) return B > 32 ? 4 : 5;
+  if (B > 128) return 0;
+  if (B > 64) return 1;
+  return B > 32 ? 2 : 3;
 }
 int head_tile_rows(int tile) { return kTiles[tile].rows; }
 int head_tile_cols(int tile) { return kTiles[tile].cols; }
@@ -200,13 +272,12 @@ void launch_head_gemm(const HeadArgs& h, int tile, hipStream_t st) {
   const TileShape t = kTiles[tile];
   const dim3 grid((h.col1 - h.col0 + t.cols - 1) / t.cols, (h.B + t.rows - 1) / t.rows);
   switch (tile) {
-    case 0: hipLaunchKernelGGL((k_head_gemm<2, 4, 4, 1>), grid, dim3(256), 0, st, h); break;
-    case 1: hipLaunchKernelGGL((k_head_gemm<1, 4, 4, 1>), grid, dim3(256), 0, st, h); break;
-    case 2: hipLaunchKernelGGL((k_head_gemm<1, 2, 2, 2>), grid, dim3(256), 0, st, h); break;
-    case 3: hipLaunchKernelGGL((k_head_gemm<1, 1, 1, 4>), grid, dim3(256), 0, st, h); break;
-    case 4: hipLaunchKernelGGL((k_head_gemm<2, 1, 4, 1>), grid, dim3(256), 0, st, h); break;
-    case 5: hipLaunchKernelGGL((k_head_gemm<1, 1, 4, 1>), grid, dim3(256), 0, st, h); break;
-    default: hipLaunchKernelGGL((k_head_gemm<1, 1, 2, 2>), grid, dim3(256), 0, st, h); break;
+    case 0: hipLaunchKernelGGL((k_head_gemm<2, 2, 4, 2, 4>), grid, dim3(512), 0, st, h); break;
+    case 1: hipLaunchKernelGGL((k_head_gemm<1, 2, 4, 2, 4>), grid, dim3(512), 0, st, h); break;
+    case 2: hipLaunchKernelGGL((k_head_gemm<1, 1, 2, 4, 4>), grid, dim3(512), 0, st, h); break;
+    case 3: hipLaunchKernelGGL((k_head_gemm<1, 1, 1, 4, 4>), grid, dim3(256), 0, st, h); break;
+    case 4: hipLaunchKernelGGL((k_head_gemm<1, 1, 2, 1, 4>), grid, dim3(128), 0, st, h); break;
+    default: hipLaunchKernelGGL((k_head_gemm<1, 1, 1, 1, 4>), grid, dim3(64), 0, st, h); break;
   }
 }
 

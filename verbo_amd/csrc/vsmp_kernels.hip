@@ -3523,6 +3523,7 @@ constexpr int kHbNT = 256;
 constexpr int kHbPer = kHeadProbe / kHbNT;  // probe logits per thread
 constexpr int kHfNT = 256;
 constexpr int kHfSmall = 2 * kHfNT;         // lists the finish ranks by counting
+constexpr int kHfPF = 8;                    // candidate loads in flight per finish thread
 static_assert(kHeadRound + kKmax <= kMergeCap && kEpiWs + kKmax <= kHeadRound + kKmax, "finish buffer");
 
 // The bin (of 2048, counts in hist) that holds the k-th largest entry, bins counted from the top
@@ -3577,7 +3578,6 @@ __global__ __launch_bounds__(kHbNT) void k_head_bound(KArgs a, HeadArgs h, const
     if (tid == 0) {
       rmode[row] = 2;
       tk[row] = 0xFFFFFFFFu;
-      h.cnt[row] = 0;
     }
     return;
   }
@@ -3590,6 +3590,14 @@ __global__ __launch_bounds__(kHbNT) void k_head_bound(KArgs a, HeadArgs h, const
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
   const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
+  // the probe's logits are loaded first, so that their loads overlap the bitmap's
+  const float* rp = probe + static_cast<long long>(row) * pld;
+  float raw[kHbPer];
+#pragma unroll
+  for (int j = 0; j < kHbPer; ++j) {
+    const int e = tid + j * kHbNT;
+    raw[j] = e < n0 ? rp[e] : 0.0f;
+  }
   for (int i = tid; i < kHeadProbe / 32; i += kHbNT) bits[i] = 0u;
   for (int i = tid; i < 2048; i += kHbNT) hist[i] = 0u;
   if (tid == 0) scnt = 0;
@@ -3601,14 +3609,11 @@ __global__ __launch_bounds__(kHbNT) void k_head_bound(KArgs a, HeadArgs h, const
     }
   }
   __syncthreads();
-  // -- the probe's logits: raw (for the candidates) and penalised order keys (for the bound)
-  const float* rp = probe + static_cast<long long>(row) * pld;
-  float raw[kHbPer];
+  // -- raw logits (for the candidates) and penalised order keys (for the bound)
   uint32_t key[kHbPer];
 #pragma unroll
   for (int j = 0; j < kHbPer; ++j) {
     const int e = tid + j * kHbNT;
-    raw[j] = e < n0 ? rp[e] : 0.0f;
     const bool hb = pen && e < n0 && ((bits[e >> 5] >> (e & 31)) & 1u);
     key[j] = e < n0 ? ord_key(hb ? penalise(raw[j], P.repeat) : raw[j]) : 0u;
   }
@@ -3639,7 +3644,8 @@ __global__ __launch_bounds__(kHbNT) void k_head_bound(KArgs a, HeadArgs h, const
     const uint32_t kl = ord_key(tl);
     tlo = min(T, kl > 8u ? kl - 8u : 0u);
   }
-  // -- the probe's candidates
+  // -- the probe's candidates (one LDS counter: the workgroup is the row's only writer)
+  unsigned long long* cr = h.rcand + static_cast<long long>(row) * h.rcap;
 #pragma unroll
   for (int j = 0; j < kHbPer; ++j) {
     const int e = tid + j * kHbNT;
@@ -3650,15 +3656,12 @@ __global__ __launch_bounds__(kHbNT) void k_head_bound(KArgs a, HeadArgs h, const
       int base = 0;
       if (lane == 0) base = atomicAdd(&scnt, __popcll(m));
       base = __shfl(base, 0);
-      if (pass) {
-        const long long pos = base + __popcll(m & ((1ull << lane) - 1ull));
-        h.cand[static_cast<long long>(row) * h.cap + pos] = comp(rk, static_cast<uint32_t>(e));
-      }
+      if (pass) cr[base + __popcll(m & ((1ull << lane) - 1ull))] = comp(rk, static_cast<uint32_t>(e));
     }
   }
   __syncthreads();
+  if (tid == 0) h.rcnt[row] = scnt;  // the main product appends after these
   if (tid == 0) {
-    h.cnt[row] = scnt;
     tk[row] = tlo;
     rmode[row] = static_cast<uint8_t>(1u | (write_all ? 2u : 0u));
   }
@@ -3747,13 +3750,23 @@ __global__ __launch_bounds__(kHfNT) void k_head_finish(KArgs a, HeadArgs h) {
     if (a.pen_bits) store_pen_words<kHfNT>(a, row, 0, bits, words);
   }
   const int n_pen = static_cast<int>(block_sum_u32<kHfNT>(np, red32));
-  const long long cap = h.cap;
-  const int n = static_cast<int>(min(static_cast<long long>(h.cnt[row]), cap));
-  const uint64_t* list = reinterpret_cast<const uint64_t*>(h.cand) + static_cast<long long>(row) * cap;
+  // the row's candidates: its list holds n of them (the probe's, then the main product's)
+  const int n = static_cast<int>(min(static_cast<long long>(h.rcnt[row]), h.rcap));
+  const uint64_t* list = reinterpret_cast<const uint64_t*>(h.rcand) + static_cast<long long>(row) * h.rcap;
 
   if (path == kPathGreedy) {  // src/sampler.cpp:66-70: the first maximum
     uint64_t b = 0ull;
-    for (int i = tid; i < n; i += kHfNT) b = max64(b, head_pen(list[i], pen, bits, P.repeat));
+    for (int i0 = 0; i0 < n; i0 += kHfNT * kHfPF) {
+      uint64_t v[kHfPF];
+#pragma unroll
+      for (int u = 0; u < kHfPF; ++u) {
+        const int i = i0 + u * kHfNT + tid;
+        v[u] = i < n ? list[i] : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < kHfPF; ++u)
+        if (i0 + u * kHfNT + tid < n) b = max64(b, head_pen(v[u], pen, bits, P.repeat));
+    }
     b = block_max64<kHfNT>(b, red64);
     if (tid == 0) {
       const int id = comp_idx(b);
@@ -3773,19 +3786,29 @@ __global__ __launch_bounds__(kHfNT) void k_head_finish(KArgs a, HeadArgs h) {
     return;
   }
 
-  // -- the exact top-k, in rounds of kHeadRound candidates: each round adds the candidates above the
-  // k-th composite so far to the k kept from the rounds before
+  // -- the exact top-k, in rounds of at most kHeadRound candidates (one round unless the row has
+  // more): each round adds its candidates above the k-th composite so far to the k kept before
   const int k = top_k_of(P, V);
   int have = 0;
   uint64_t bound = 0ull;
   int kk = 0;
   for (int base = 0; base < n; base += kHeadRound) {
-    const int mr = min(kHeadRound, n - base);
+    const int end = min(n, base + kHeadRound);
     if (tid == 0) sint[3] = 0;
     __syncthreads();
-    for (int i = tid; i < mr; i += kHfNT) {
-      const uint64_t c = head_pen(list[base + i], pen, bits, P.repeat);
-      if (c > bound) buf[have + atomicAdd(&sint[3], 1)] = c;
+    for (int i0 = base; i0 < end; i0 += kHfNT * kHfPF) {  // kHfPF loads in flight per thread
+      uint64_t v[kHfPF];
+#pragma unroll
+      for (int u = 0; u < kHfPF; ++u) {
+        const int i = i0 + u * kHfNT + tid;
+        v[u] = i < end ? list[i] : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < kHfPF; ++u) {
+        if (i0 + u * kHfNT + tid >= end) continue;
+        const uint64_t x = head_pen(v[u], pen, bits, P.repeat);
+        if (x > bound) buf[have + atomicAdd(&sint[3], 1)] = x;
+      }
     }
     __syncthreads();
     const int m = have + sint[3];
