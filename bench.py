@@ -207,7 +207,7 @@ def bench_head(args):
 
     import verbo_amd as V
 
-    B, Vv, D, H = 256, 151936, 896, 512
+    B, Vv, D, H = args.head_rows, 151936, 896, 512
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
@@ -252,7 +252,14 @@ def bench_head(args):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / args.steps
 
-    ms = {name: timed(fn) for name, fn in (("fused", fused), ("unfused", unfused), ("product", product))}
+    lib_out = torch.empty(B, Vv, dtype=torch.bfloat16, device=dev)
+
+    def library(i, st):  # the vendor library's product of the same operands (bf16 out), for reference
+        with torch.cuda.stream(st):
+            torch.nn.functional.linear(hidden, heads[i % 3], out=lib_out)
+
+    ms = {name: timed(fn) for name, fn in (("fused", fused), ("unfused", unfused), ("product", product),
+                                           ("library", library))}
     for k_, v in ms.items():
         log(f"[bench] head: {k_} {v * 1e3:.1f} us/step")
     head_bytes = Vv * D * 2
@@ -260,7 +267,7 @@ def bench_head(args):
     achieved = alg / (ms["fused"] * 1e-3) / 1e9
     flops = 2.0 * B * Vv * D
     return {
-        "metric": f"sampled rows/s, {DESCR['head']}",
+        "metric": f"sampled rows/s, {DESCR['head']}".replace("256 x 896", f"{B} x 896"),
         "value": B / (ms["fused"] * 1e-3),
         "unit": "rows/s",
         "n_gpus": 1,
@@ -272,9 +279,11 @@ def bench_head(args):
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": DESCR["head"], "B": B, "V": Vv, "D": D, "head_copies": 3,
+        "config": {"workload": DESCR["head"].replace("256 x 896", f"{B} x 896"), "B": B, "V": Vv, "D": D,
+                   "head_copies": 3,
                    "algorithmic_bytes_per_step": alg, "issue": "hip_graph",
                    "unfused_ms_per_step": ms["unfused"], "product_ms_per_step": ms["product"],
+                   "library_product_bf16_ms_per_step": ms["library"],
                    "mfma_tflops_fused": flops / (ms["fused"] * 1e-3) / 1e12,
                    "mfma_tflops_product": flops / (ms["product"] * 1e-3) / 1e12},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -303,6 +312,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0: skip)")
     ap.add_argument("--min-buffer-mb", type=float, default=640.0)
     ap.add_argument("--draws", type=int, default=10000, help="single workload: consecutive draws timed")
+    ap.add_argument("--head-rows", type=int, default=256, help="head workload: rows (hidden states) per call")
     ap.add_argument("--eager", action="store_true", help="issue the timed calls one by one instead of from a HIP graph")
     ap.add_argument("--copy", action="store_true",
                     help="time a plain device copy of one logits buffer per step instead (the known-size kernel "

@@ -3519,10 +3519,10 @@ __global__ __launch_bounds__(256) void k_numer_probe(const float* __restrict__ d
 // penalises those candidates, takes the exact top-k and runs the reference epilogue. The logits of
 // such rows are never written unless the caller asks for them.
 
-constexpr int kHbNT = 256;
+constexpr int kHbNT = 1024;
 constexpr int kHbPer = kHeadProbe / kHbNT;  // probe logits per thread
-constexpr int kHfNT = 256;
-constexpr int kHfSmall = 2 * kHfNT;         // lists the finish ranks by counting
+constexpr int kHfNT = 1024;
+constexpr int kHfSmall = 512;              // lists the finish ranks by counting
 constexpr int kHfPF = 8;                    // candidate loads in flight per finish thread
 static_assert(kHeadRound + kKmax <= kMergeCap && kEpiWs + kKmax <= kHeadRound + kKmax, "finish buffer");
 
