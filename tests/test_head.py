@@ -229,3 +229,36 @@ def test_head_bad_arguments(ctx):
         ctx.head_logits(hidden, head[:, :32].contiguous())
     with pytest.raises(V.VsmpError, match="ldl"):
         ctx.head_pick(hidden, head, V.Params(), logits=torch.zeros((4, 999), device="cuda"))
+
+
+def test_head_pick_row_tiles_padding_and_draw_modes(ctx):
+    """300 rows (two row tiles of the main product, five of the probe), padded leading dimensions,
+    and the device draw modes: with xorshift draws (the reference's stream, advanced in place) and
+    with counter draws, the fused pick equals vsmp_pick_batch on the head's logits, and the streams
+    end in the same state."""
+    import torch
+
+    B, Vv, D = 300, 9000, 192
+    hidden_w, head_w = operands(31, B, Vv, D + 64)
+    hidden = hidden_w[:, :D]  # row stride D + 64
+    head = head_w[:, :D]
+    logits = ctx.head_logits(hidden, head)
+    rng = np.random.default_rng(12)
+    hist, off = csr([rng.integers(0, Vv, int(rng.integers(0, 80))) for _ in range(B)])
+    dh, dho = torch.from_numpy(hist).cuda(), torch.from_numpy(off).cuda()
+    for p in (dict(temp=0.9, top_k=40, top_p=0.9, min_p=0.02, repeat=1.15, repeat_last=32, seed=8),
+              dict(temp=0.0, repeat=1.2, repeat_last=16, seed=8)):
+        prm = V.Params(*[V.params_array(n=1, **p)[0][f].item() for f in V.SAMPLING_DTYPE.names])
+        state = torch.from_numpy(rng.integers(1, 1 << 62, 2 * B).astype(np.int64)).cuda()
+        s1, s2 = state.clone(), state.clone()
+        a = ctx.head_pick(hidden, head, prm, dh, dho, V.U_XORSHIFT, rng_state=s1)
+        b = ctx.pick_batch(logits, prm, dh, dho, V.U_XORSHIFT, rng_state=s2)
+        torch.cuda.synchronize()
+        assert np.array_equal(a.cpu().numpy(), b.cpu().numpy()), p
+        assert np.array_equal(s1.cpu().numpy(), s2.cpu().numpy()), p
+    per_row = V.to_device_params(V.params_array(
+        [dict(temp=0.7 + 0.001 * r, top_k=[0, 20, 300, 1][r % 4], top_p=0.9, repeat=1.1, seed=r) for r in range(B)]))
+    a = ctx.head_pick(hidden, head, per_row, dh, dho, V.U_COUNTER, counter=5)
+    b = ctx.pick_batch(logits, per_row, dh, dho, V.U_COUNTER, counter=5)
+    torch.cuda.synchronize()
+    assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
