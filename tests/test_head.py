@@ -50,7 +50,7 @@ def fp32_reference(hidden, head):
 
 
 @pytest.mark.parametrize("B,Vv,D", [(1, 1000, 64), (37, 4099, 128), (130, 5000, 192), (64, 8269, 256),
-                                    (256, 20000, 896)])
+                                    (256, 20000, 896), (8, 5000, 4096)])
 def test_head_logits_match_fp32_product(ctx, B, Vv, D):
     """Every logit within 2e-5 of sum |x_d w_d| of the fp32 product: the fp32 accumulation of D
     exact bf16 products in another order (and one that swaps rows or columns is off by far more)."""
