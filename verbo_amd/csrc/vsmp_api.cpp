@@ -375,7 +375,7 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
   const bool exact = exact_scratch && (params_per_row || (params->top_p > 0.0f && params->top_p < 1.0f));
   if (exact_scratch && (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch", busy) ||
                         !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch", busy) ||
-                        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(exact_slots(a.x_n)) * 2 * a.x_n, false, "scratch",
+                        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(exact_slots(a.x_n, B)) * 2 * a.x_n, false, "scratch",
                               busy)))
     return -1;
   if (pl.any_general && !pl.rows && !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch", busy))
@@ -420,7 +420,7 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
     launch_general(a, ctx->side);
     bool ok = hip_ok(hipGetLastError(), "general-path launch");
     if (ok && exact) {
-      launch_general_exact(a, exact_slots(a.x_n), ctx->side);
+      launch_general_exact(a, exact_slots(a.x_n, B), ctx->side);
       ok = hip_ok(hipGetLastError(), "exact general-path launch");
     }
     if (!hip_ok(hipEventRecord(ctx->join_ev, ctx->side), "hipEventRecord")) return -1;
@@ -449,7 +449,7 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
     launch_general(a, st);
     if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
     if (exact) {
-      launch_general_exact(a, exact_slots(a.x_n), st);
+      launch_general_exact(a, exact_slots(a.x_n, B), st);
       if (!hip_ok(hipGetLastError(), "exact general-path launch")) return -1;
     }
   }
@@ -618,14 +618,14 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
   if (params_per_row) {
     if (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch", busy) ||
         !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch", busy) ||
-        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(exact_slots(a.x_n)) * 2 * a.x_n, false, "scratch", busy))
+        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(exact_slots(a.x_n, B)) * 2 * a.x_n, false, "scratch", busy))
       return -1;
     a.x_flag = ctx->x_flag;
     a.x_u = ctx->x_u;
     a.x_buf = ctx->x_buf;
     launch_general(a, st);
     if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
-    launch_general_exact(a, exact_slots(a.x_n), st);
+    launch_general_exact(a, exact_slots(a.x_n, B), st);
     if (!hip_ok(hipGetLastError(), "exact general-path launch")) return -1;
   }
   return 0;

@@ -59,7 +59,7 @@ struct KArgs {
   int words;                   // bitmap words per row
   // general rows whose top-p cut lay within rounding distance of top_p: k_general marks them
   // (x_flag) with the draw it used (x_u), and k_general_exact redoes them in the reference's order
-  // and sequential sums, sorting each in one of exact_slots(x_n) scratch slots of 2 * x_n entries
+  // and sequential sums, sorting each in one of exact_slots(x_n, B) scratch slots of 2 * x_n entries
   int* x_flag;
   double* x_u;
   unsigned long long* x_buf;
@@ -82,12 +82,15 @@ void launch_rows(const KArgs& a, hipStream_t st);
 void launch_general(const KArgs& a, hipStream_t st);
 void launch_general_exact(const KArgs& a, int slots, hipStream_t st);
 void launch_numer_probe(const float* d, double* y, long long n, float temp, float qs, hipStream_t st);
-// Workgroups (and scratch slots of 2 * x_n entries) of k_general_exact: as many as 256 MB of slots
-// hold, between 8 and 32 (32 slots of 4 MB at 151,936 logits).
-inline int exact_slots(int x_n) {
+// Workgroups (and scratch slots of 2 * x_n entries) of k_general_exact for a batch of B rows: one
+// per row up to 256 (one per CU, so that a batch whose rows are all marked is redone in parallel),
+// at least 8, within 1 GB of slots (256 slots of 4 MB at 151,936 logits, 64 of 16 MB at 2^20).
+inline int exact_slots(int x_n, int B) {
   const long long per = 16LL * x_n;
-  const long long n = (256LL << 20) / per;
-  return static_cast<int>(n < 8 ? 8 : (n > 32 ? 32 : n));
+  const long long budget = (1LL << 30) / per;
+  long long n = B < 8 ? 8 : (B > 256 ? 256 : B);
+  if (n > budget) n = budget;
+  return static_cast<int>(n < 1 ? 1 : n);
 }
 constexpr int kExactMaxVocab = kMaxVocab; // k_general_exact's reach: every row a call accepts
 
