@@ -21,9 +21,10 @@
 //            slice maximum; small-k rows (k <= 256) also write the slice's exact, sorted top-k.
 //  k_finish  one workgroup per greedy / small-k row after k_stage1: merges the slice results and
 //            runs the epilogue.
-//  k_general one workgroup per remaining row (k > 256 or top-k off): a mass histogram of the fp64
-//            numerators, then count and mass selects over the row, with histograms in LDS. In row
-//            mode it takes the row's maximum pass and penalty bitmap itself.
+//  k_general one workgroup per remaining row (k > 256 or top-k off): a count and mass histogram of
+//            the numerators (fixed-point sums per bucket), then count and mass selects over the
+//            row, with histograms in LDS. In row mode it takes the row's maximum pass and penalty
+//            bitmap itself.
 //  k_general_exact  after k_general: the rows it marked (a top-p cut at rounding distance of
 //            top_p) redone in the reference's order and sequential sums.
 //  k_read_probe  a plain streaming read, for the attainable-bandwidth measurement.
@@ -47,7 +48,10 @@ constexpr double kNearTopP = 1e-11;  // |acc - top_p| below this: reference roun
 // The general path's bound on that distance for a prefix of k numerators: its sums run in bucket
 // order, and a sum of k non-negative terms in any order lies within (k - 1) * 2^-53 of the exact
 // sum (relative), as does the reference's sequential one; the band is four times that, and never
-// below kNearTopP.
+// below kNearTopP. The level-0 bucket masses round each term to 2^-41 of its value at most (fixed
+// point, numer_fix), which moves a prefix over the total by under 2^-40 = 9.1e-13: inside the band,
+// whose excess over 2 (k - 1) 2^-53 is at least 1e-11 - 2^-38 below k = 22,518 and 2 k 2^-53 >= 5e-12
+// above it.
 __device__ __forceinline__ double near_topp(int k) { return fmax(kNearTopP, 4.0 * static_cast<double>(k) * kTwoM53); }
 constexpr double kNearMinP = 1e-13;  // |pr - thr| / thr below this: exp last-bit territory
 constexpr double kNearDraw = 1e-6;   // draws this close to a CDF boundary are reported
@@ -1402,6 +1406,24 @@ __device__ __forceinline__ double numer_tab(const GenCtx& g, const double* etab,
   return fma(e * r, s, e);
 }
 
+// The main pass's mass of an element of bucket q relative to its table point: exp(x - c_(q >> 1))
+// (within e^(+-1/64) of 1) as a fixed-point integer of 2^-40 units, rounded to nearest by one fma
+// (4097 + r s has a 2^-40 ulp; its low 52 bits are the value's). Bucket q's mass is then
+// etab[q >> 1] * sum * 2^-40: each term within 2^-41 (relative, times e^(1/64)) of numer_tab's, and
+// the sums exact and order-free (at most 2^20 terms of under 2^40.03 each).
+__device__ __forceinline__ uint64_t numer_fix(const GenCtx& g, double w, float d, int q) {
+  const double x = static_cast<double>(d) * g.inv_temp;
+  const double r = fma(static_cast<double>(q | 1), w, x);
+  double s = fma(r, 0x1.6c16c16c16c17p-10, 0x1.1111111111111p-7);  // 1/720, 1/120
+  s = fma(r, s, 0x1.5555555555555p-5);                              // 1/24
+  s = fma(r, s, 0x1.5555555555555p-3);                              // 1/6
+  s = fma(r, s, 0.5);
+  s = fma(r, s, 1.0);
+  const double t = fma(r, s, 4097.0);
+  return static_cast<uint64_t>(__double_as_longlong(t)) & ((1ull << 52) - 1ull);
+}
+constexpr double kFixUnit = 0x1p-40;
+
 // atomicMin(dst, i) for the lane of this wave whose claim holds with the smallest lane index (the
 // callers' positions grow with the lane index): one LDS atomic per wave instead of one per lane,
 // where thousands of lanes can claim.
@@ -1728,19 +1750,27 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     g.ckk = s.ck;
   }
 
-  // pass: sum over the top-k prefix, min-p statistics, level-0 mass histogram
+  // pass: min-p statistics, level-0 count and mass histograms (the masses as fixed-point sums
+  // relative to the table points, numer_fix, in the mass array's 8-byte slots until the prefix
+  // below turns them into fp64 masses)
+  uint64_t* fix0 = reinterpret_cast<uint64_t*>(sh.mass0);
   for (int i = tid; i < kGenBuckets; i += kGenThreads) {
     sh.cnt0[i] = 0u;
-    sh.mass0[i] = 0.0;
+    fix0[i] = 0ull;
   }
-  // the main pass's table (numer_tab), in the refinement histograms, which are free until it ends
+  // the main pass's table (numer_tab), in the refinement histograms, which are free until the
+  // prefix below has used it
   double* etab = sh.rmass;
   const double wq = table_width(g.qs, P.temp);
   for (int j = tid; j < kGenBuckets / 2; j += kGenThreads) etab[j] = exp_tab(-static_cast<double>(2 * j + 1) * wq);
   __syncthreads();
   const bool minp = P.min_p > 0.0f;
   const double thr = static_cast<double>(P.min_p);  // pr of the maximum is exactly 1
-  double t_sum = 0.0, t_totm = 0.0, t_omass = 0.0;
+  // A floor under d = v - mx (the float the numerators take) for every element whose numerator can
+  // reach thr, d / temp >= log(thr) (exp within 1e-15): the exact numerator is taken only above it.
+  const float dmin = minp ? static_cast<float>(static_cast<double>(P.temp) * log(thr) * 1.001) - 1e-3f : INFINITY;
+  double t_totm = 0.0, t_omass = 0.0;
+  uint64_t t_ofix = 0ull;
   uint32_t t_cntm = 0, t_ocnt = 0;
   const bool cut_k = g.ckk != 0ull;
   // The overflow bucket of a capped row holds elements at least 63.98 temp below the maximum, whose
@@ -1754,22 +1784,30 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     auto excluded = [&](int e, float v) {
       return decltype(with_cut)::value && cut_k && comp(ord_key(v), static_cast<uint32_t>(e)) < g.ckk;
     };
-    auto add = [&](float v, int q, double p) {
+    auto add = [&](float v, float d, int q, uint64_t f) {
       if (decltype(ovf)::value && q == kGenBuckets - 1) {
         ++t_ocnt;
         if (capped) {
           if (!ovf_exact) return;
-          p = numer_g(g, v);
+          const double p = numer_g(g, v);
+          t_omass += p;
+          if (decltype(with_minp)::value && p >= thr) {
+            ++t_cntm;
+            t_totm += p;
+          }
+          return;
         }
-        t_omass += p;
+        t_ofix += f;
       } else {
         atomicAdd(&sh.cnt0[q], 1u);
-        atomicAdd(&sh.mass0[q], p);
+        atomicAdd(&fix0[q], f);
       }
-      t_sum += p;
-      if (decltype(with_minp)::value && minp && p >= thr) {
-        ++t_cntm;
-        t_totm += p;
+      if (decltype(with_minp)::value && d >= dmin) {
+        const double p = numer_tab(g, etab, wq, d, q);
+        if (p >= thr) {
+          ++t_cntm;
+          t_totm += p;
+        }
       }
     };
     gen_pass_groups<1>(
@@ -1777,22 +1815,22 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
         [&](int e, float v) {
           const float d = v - g.mx;
           const int q = q_of_d(g, d);
-          if (!excluded(e, v)) add(v, q, numer_tab(g, etab, wq, d, q));
+          if (!excluded(e, v)) add(v, d, q, numer_fix(g, wq, d, q));
         },
-        // the four numerators first: their table reads then go out together, ahead of the
-        // histogram atomics (LDS writes, which later LDS reads may not pass)
+        // the four masses first, then the four elements' histogram atomics together
         [&](int e, const float (&x)[4]) {
           int q[4];
-          double p[4];
+          float d[4];
+          uint64_t f[4];
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
-            const float d = x[c] - g.mx;
-            q[c] = q_of_d(g, d);
-            p[c] = numer_tab(g, etab, wq, d, q[c]);
+            d[c] = x[c] - g.mx;
+            q[c] = q_of_d(g, d[c]);
+            f[c] = numer_fix(g, wq, d[c], q[c]);
           }
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            if (!excluded(e + c, x[c])) add(x[c], q[c], p[c]);
+            if (!excluded(e + c, x[c])) add(x[c], d[c], q[c], f[c]);
         });
   };
   // one instance per combination without a top-k restriction (the common case: no per-element
@@ -1810,13 +1848,14 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   {
     const uint32_t oc = block_sum_u32<kGenThreads>(t_ocnt, sh.r32);
     const double om = block_sum_f64<kGenThreads>(t_omass, sh.rd);
+    for (int o = 32; o > 0; o >>= 1) t_ofix += __shfl_xor(t_ofix, o);
+    if ((tid & 63) == 0 && t_ofix != 0ull) atomicAdd(&fix0[kGenBuckets - 1], t_ofix);
     if (tid == 0) {
       sh.cnt0[kGenBuckets - 1] += oc;
-      sh.mass0[kGenBuckets - 1] += om;
+      sh.dbls[2] = om;  // the capped overflow bucket's fp64 mass
     }
     __syncthreads();
   }
-  const double sum = block_sum_f64<kGenThreads>(t_sum, sh.rd);
   double totm = 0.0;
   uint32_t cntm = 0;
   if (minp) {
@@ -1846,8 +1885,10 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     uint32_t cs = 0;
 #pragma unroll
     for (int i = 0; i < BP; ++i) {
-      m[i] = sh.mass0[b0 + i];
-      c[i] = sh.cnt0[b0 + i];
+      const int b = b0 + i;
+      m[i] = etab[b >> 1] * (static_cast<double>(fix0[b]) * kFixUnit);
+      if (b == kGenBuckets - 1) m[i] += sh.dbls[2];
+      c[i] = sh.cnt0[b];
       ms += m[i];
       cs += c[i];
     }
@@ -1863,6 +1904,8 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     }
     __syncthreads();
   }
+  // the sum over the top-k prefix (src/sampler.cpp:84): the histogram's total
+  const double sum = sh.mass0[kGenBuckets - 1];
 
   // src/sampler.cpp:86-91 (min-p), with the count of a prefix
   int keep = k;
