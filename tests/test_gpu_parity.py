@@ -549,6 +549,46 @@ def test_topk_split_parts(dmode):
         assert (dst.cpu().numpy().view(np.uint64) == st).all()
 
 
+@pytest.mark.parametrize("kind", ["topp", "minp", "topk", "capped", "capped_minp", "flat"])
+def test_general_path_two_workgroups_per_cu(kind):
+    """Shared-parameter batches of general rows without a penalty and with more rows than the device
+    has CUs run on two 512-thread workgroups per CU (the wide workload's launch): top-p, min-p, a
+    top-k restriction above 256, rows wider than the buckets' 64 temp (capped, with and without a
+    min-p threshold small enough to keep the overflow bucket) and tied rows that the exact redo
+    takes; every comparison of the parity bar against the oracle."""
+    import torch
+
+    ctx = mode_ctx("rows")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rng = np.random.default_rng({"topp": 91, "minp": 92, "topk": 93, "capped": 94, "capped_minp": 95, "flat": 96}[kind])
+    B, Vv = cus + 37, 5003
+    lg = rng.normal(0.0, 1.0, (B, Vv))
+    prm = dict(temp=1.0, top_k=0, top_p=0.9, min_p=0.0, repeat=1.0, repeat_last=0, seed=int(rng.integers(1, 1 << 62)))
+    if kind == "minp":
+        lg[:, rng.integers(0, Vv, 8)] += 5.0
+        prm.update(temp=0.7, top_p=0.95, min_p=0.05)
+    elif kind == "topk":
+        prm.update(top_k=1000, top_p=0.9)
+    elif kind == "capped":
+        lg = rng.normal(0.0, 40.0, (B, Vv))
+        prm.update(temp=0.5, top_p=0.99)
+    elif kind == "capped_minp":
+        lg = rng.normal(0.0, 40.0, (B, Vv))
+        prm.update(temp=0.5, top_p=0.99, min_p=1e-30)
+    elif kind == "flat":
+        Vv = 5004
+        lg = np.zeros((B, Vv))
+        prm.update(top_p=0.5)
+    p = V.params_array(n=1, **prm)
+    h, off = csr([list(rng.integers(0, Vv, 50)) for _ in range(B)])  # ignored: repeat 1
+    log("two workgroups per CU", kind, B, Vv)
+    run = Run(ctx, lg.astype(np.float32), p, h, off, cand_cap=128)
+    run.report()
+    assert (run.info["path"] == V.PATH_GENERAL).all()
+    if kind == "flat":
+        assert (run.info["flags"] & V.FLAG_SEQ_CUTS).all(), run.info["flags"]
+
+
 def test_general_path_all_rows_marked(ctx):
     """Every row of a batch goes to the exact redo: 40 rows of 151,936 equal logits with top-p 0.5
     (the top-p sum meets top_p exactly at an even count), a third with a penalised history, on the

@@ -417,7 +417,7 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
     if (!hip_ok(hipEventRecord(ctx->fork_ev, st), "hipEventRecord") ||
         !hip_ok(hipStreamWaitEvent(ctx->side, ctx->fork_ev, 0), "hipStreamWaitEvent"))
       return -1;
-    launch_general(a, ctx->side);
+    launch_general(a, ctx->cus, ctx->side);
     bool ok = hip_ok(hipGetLastError(), "general-path launch");
     if (ok && exact) {
       launch_general_exact(a, exact_slots(a.x_n, B), ctx->side);
@@ -446,7 +446,7 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
     if (!hip_ok(hipGetLastError(), "finish launch")) return -1;
   }
   if (pl.any_general) {
-    launch_general(a, st);
+    launch_general(a, ctx->cus, st);
     if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
     if (exact) {
       launch_general_exact(a, exact_slots(a.x_n, B), st);
@@ -623,7 +623,7 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
     a.x_flag = ctx->x_flag;
     a.x_u = ctx->x_u;
     a.x_buf = ctx->x_buf;
-    launch_general(a, st);
+    launch_general(a, ctx->cus, st);
     if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
     launch_general_exact(a, exact_slots(a.x_n, B), st);
     if (!hip_ok(hipGetLastError(), "exact general-path launch")) return -1;
@@ -670,7 +670,7 @@ int pick_batch_noalloc(const float* logits, int B, int V, long long ld, const vs
     if (!hip_ok(hipGetLastError(), "row launch")) return -1;
   }
   if (any_general) {
-    launch_general(a, st);
+    launch_general(a, 0, st);  // 1024-thread workgroups (no device query here)
     if (!hip_ok(hipGetLastError(), "general-path launch")) return -1;
     if (exact) {
       launch_general_exact(a, 1, st);  // one sort slot: marked rows are redone one after another

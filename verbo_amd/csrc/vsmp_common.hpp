@@ -79,7 +79,8 @@ constexpr int kSplitMaxPartGroups = 4096;  // 16-byte groups one split part load
 void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st);
 void launch_finish(const KArgs& a, hipStream_t st);
 void launch_rows(const KArgs& a, hipStream_t st);
-void launch_general(const KArgs& a, hipStream_t st);
+// cus: the device's CUs (0: unknown), which sets the workgroup size for large general batches.
+void launch_general(const KArgs& a, int cus, hipStream_t st);
 void launch_general_exact(const KArgs& a, int slots, hipStream_t st);
 void launch_numer_probe(const float* d, double* y, long long n, float temp, float qs, hipStream_t st);
 // Workgroups (and scratch slots of 2 * x_n entries) of k_general_exact for a batch of B rows: one

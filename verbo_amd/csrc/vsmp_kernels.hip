@@ -1179,7 +1179,6 @@ __global__ __launch_bounds__(kTpb) void k_finish(KArgs a) {
 
 // ---- general path -------------------------------------------------------------------------------
 
-constexpr int kGenNW = kGenThreads / 64;
 constexpr int kRefBuckets = 2048;
 static_assert(kGenBuckets % kGenThreads == 0 && kRefBuckets % kGenThreads == 0, "whole buckets per thread");
 static_assert(kGenCap <= 2 * kGenThreads, "lists of up to kGenCap entries are scanned two per thread");
@@ -1206,8 +1205,9 @@ __device__ __forceinline__ uint32_t* gen_lds_bits() {
 // loads in flight (a and b); every load is issued unconditionally (past the row it rereads the last
 // 16-byte group, which 4*ceil(V/4) <= ld keeps inside the row), so each wait covers exactly the
 // buffer about to be processed.
-template <int U, class F, class F4, class W>
+template <int NT, int U, class F, class F4, class W>
 __device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, F4&& f4, W&& word) {
+  constexpr int kGenThreads = NT;
   constexpr int step = kGenThreads * 4 * U;
   const int tid = static_cast<int>(threadIdx.x);
   const float4* rp4 = reinterpret_cast<const float4*>(R.rp);
@@ -1257,22 +1257,25 @@ __device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, F4&& f4, W
 // 16-byte group, which lets a caller order the work of four elements itself. U: 16-byte loads per
 // thread and buffer (two buffers in flight); U = 4 for the select passes measured slower (the
 // kernel's code grows by half and every phase slows), so every pass takes U = 1.
-template <int U, class F, class F4>
+template <int NT, int U, class F, class F4>
 __device__ __forceinline__ void gen_pass_groups(const GenRow& R, F&& f, F4&& f4) {
   if (R.lds_bits)
-    gen_pass_loop<U>(R, f, f4, [](int i) { return gen_lds_bits()[i]; });
+    gen_pass_loop<NT, U>(R, f, f4, [](int i) { return gen_lds_bits()[i]; });
   else
-    gen_pass_loop<U>(R, f, f4, [&R](int i) { return R.bits[i]; });
+    gen_pass_loop<NT, U>(R, f, f4, [&R](int i) { return R.bits[i]; });
 }
-template <int U = 1, class F>
+template <int NT, int U = 1, class F>
 __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
-  gen_pass_groups<U>(R, f, [&f](int e, const float (&x)[4]) {
+  gen_pass_groups<NT, U>(R, f, [&f](int e, const float (&x)[4]) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) f(e + c, x[c]);
   });
 }
 
+// k_general's LDS for a workgroup of NT threads (kGenNW waves).
+template <int NT>
 struct __align__(16) GenShared {  // list is read as 16-byte vectors
+  static constexpr int kGenNW = NT / 64;
   uint32_t cnt0[kGenBuckets];   // level-0 inclusive prefix counts (by mass bucket q)
   double mass0[kGenBuckets];    // level-0 inclusive prefix masses
   union {                       // a refinement's histograms, then the elements it collects
@@ -1442,7 +1445,9 @@ constexpr int kGenRankMax = 384;  // longest collected list ranked by counting (
 // Sorts list[0, m) descending (block-wide; the composites are distinct). Short lists: each entry's
 // rank by counting, placed through tmp (m entries); longer ones: bitonic, with list zero-padded to a
 // power of two (the caller's list has room).
-__device__ __forceinline__ void sort_desc(GenShared& sh, uint64_t* list, uint64_t* tmp, int m) {
+template <int NT>
+__device__ __forceinline__ void sort_desc(GenShared<NT>& sh, uint64_t* list, uint64_t* tmp, int m) {
+  constexpr int kGenThreads = NT;
   const int tid = threadIdx.x;
   if (m <= kGenRankMax) {
     const int mpad = (m + 15) & ~15;
@@ -1463,16 +1468,18 @@ __device__ __forceinline__ void sort_desc(GenShared& sh, uint64_t* list, uint64_
   }
 }
 
-__device__ __forceinline__ Sel find_in_prefix(GenShared& sh, const uint64_t* list, const double* lpr, int m,
+template <int NT>
+__device__ __forceinline__ Sel find_in_prefix(GenShared<NT>& sh, const uint64_t* list, const double* lpr, int m,
                                               int rank_above, double above, double target);
 
 // The first entry of the descending list[0, m) at which the running weight, starting from `above`
 // after `rank_above` elements, reaches target. Weights are 1 (count) or the fp64 numerators (mass);
 // lpr[0, m) receives the inclusive running weights. When rounding leaves the target just past the
 // list, its last entry (found = false).
-template <bool MASS>
-__device__ __forceinline__ Sel scan_sorted(const GenCtx& g, GenShared& sh, const uint64_t* list, double* lpr, int m,
+template <bool MASS, int NT>
+__device__ __forceinline__ Sel scan_sorted(const GenCtx& g, GenShared<NT>& sh, const uint64_t* list, double* lpr, int m,
                                            int rank_above, double above, double target) {
+  constexpr int kGenThreads = NT;
   const int tid = threadIdx.x;
   const int i0 = 2 * tid, i1 = i0 + 1;
   const double w0 = i0 < m ? (MASS ? numer_g(g, comp_val(list[i0])) : 1.0) : 0.0;
@@ -1486,7 +1493,8 @@ __device__ __forceinline__ Sel scan_sorted(const GenCtx& g, GenShared& sh, const
 }
 
 // The first entry of list[0, m) whose inclusive running weight lpr reaches target (see scan_sorted).
-__device__ __forceinline__ Sel find_in_prefix(GenShared& sh, const uint64_t* list, const double* lpr, int m,
+template <int NT>
+__device__ __forceinline__ Sel find_in_prefix(GenShared<NT>& sh, const uint64_t* list, const double* lpr, int m,
                                               int rank_above, double above, double target) {
   const int tid = threadIdx.x;
   const int i0 = 2 * tid, i1 = i0 + 1;
@@ -1516,9 +1524,10 @@ __device__ __forceinline__ Sel find_in_prefix(GenShared& sh, const uint64_t* lis
 }
 
 
-template <bool MASS, class PV, class PC>
-__device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, PV&& pred_v, PC&& pred_c, uint64_t clo,
+template <bool MASS, class PV, class PC, int NT>
+__device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared<NT>& sh, PV&& pred_v, PC&& pred_c, uint64_t clo,
                                              uint64_t chi, int n, int rank_above, double above, double target) {
+  constexpr int kGenThreads = NT;
   const int tid = threadIdx.x;
   for (int level = 0; level < 8 && n > kGenCap && clo < chi; ++level) {
     const uint64_t span = chi - clo;
@@ -1530,7 +1539,7 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, PV&
     }
     __syncthreads();
     const uint32_t klo = comp_key(clo), khi = comp_key(chi);
-    gen_pass(g.R, [&](int e, float v) {
+    gen_pass<NT>(g.R, [&](int e, float v) {
       const uint32_t kv = ord_key(v);
       if (kv < klo || kv > khi || !pred_v(v)) return;
       const uint64_t ck = comp(kv, static_cast<uint32_t>(e));
@@ -1618,7 +1627,7 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, PV&
   __syncthreads();
   {
   const uint32_t klo = comp_key(clo), khi = comp_key(chi);
-  gen_pass(g.R, [&](int e, float v) {
+  gen_pass<NT>(g.R, [&](int e, float v) {
     const uint32_t kv = ord_key(v);
     if (kv < klo || kv > khi || !pred_v(v)) return;
     const uint64_t ck = comp(kv, static_cast<uint32_t>(e));
@@ -1633,8 +1642,12 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared& sh, PV&
   return scan_sorted<MASS>(g, sh, sh.list, sh.lpr, m, rank_above, above, target);
 }
 
-__global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
-  __shared__ GenShared sh;
+// NT threads per workgroup: 1024, or 512 (two workgroups per CU, each holding its row's passes
+// while the other's wait on memory) for batches with more general rows than CUs.
+template <int NT>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_general(KArgs a) {
+  constexpr int kGenThreads = NT;
+  __shared__ GenShared<NT> sh;
   const int V = a.V;
   const int tid = threadIdx.x;
   // Workgroup b takes the b-th general row. With per-row parameters the general rows are then the
@@ -1698,7 +1711,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
       if (a.pen_bits) store_pen_words<kGenThreads>(a, row, 0, lb, a.words);
     }
     uint32_t mn = 0xFFFFFFFFu;
-    gen_pass(g.R, [&](int e, float v) {
+    gen_pass<NT>(g.R, [&](int e, float v) {
       const uint32_t kv = ord_key(v);
       mxc = max64(mxc, comp(kv, static_cast<uint32_t>(e)));
       mn = min(mn, kv);
@@ -1810,7 +1823,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
         }
       }
     };
-    gen_pass_groups<1>(
+    gen_pass_groups<NT, 1>(
         g.R,
         [&](int e, float v) {
           const float d = v - g.mx;
@@ -1867,7 +1880,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
   // diagnostics. by_minp: the set is the min-p prefix (numerator >= thr), else the top-k prefix.
   auto kept_last = [&](bool by_minp) -> uint64_t {
     uint64_t t = ~0ull;
-    gen_pass(g.R, [&](int e, float v) {
+    gen_pass<NT>(g.R, [&](int e, float v) {
       const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
       if (ck < g.ckk) return;
       if (by_minp && !(numer_g(g, v) >= thr)) return;
@@ -1971,7 +1984,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     uint64_t clo = 0ull, chi = ~0ull;
     if (n > kGenCap) {  // tighten the composite range to the bucket's
       uint64_t lo_ = ~0ull, hi_ = 0ull;
-      gen_pass(g.R, [&](int e, float v) {
+      gen_pass<NT>(g.R, [&](int e, float v) {
         if (!in_q_v(v)) return;
         const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
         if (!in_q_c(ck)) return;
@@ -2019,7 +2032,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     const float vlo = g.mx + static_cast<float>(static_cast<double>(P.temp) * log(thr) * 1.001) - 1e-3f;
     if (tid == 0) sh.ints[4] = 0;
     __syncthreads();
-    gen_pass(g.R, [&](int e, float v) {
+    gen_pass<NT>(g.R, [&](int e, float v) {
       if (!(v >= vlo)) return;
       if (!(numer_g(g, v) >= thr)) return;
       const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
@@ -2067,7 +2080,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
           }
           __syncthreads();
           const uint64_t ckk = g.ckk;
-          gen_pass(g.R, [&](int e, float v) {
+          gen_pass<NT>(g.R, [&](int e, float v) {
             const int q = q_of(g, v);
             const bool inA = q == qp, inB = q >= d_lo && q <= d_hi;
             if (!inA && !inB) return;
@@ -2163,7 +2176,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general(KArgs a) {
     const uint64_t cm = s.ck;
     if (tid == 0) sh.ints[4] = 0;
     __syncthreads();
-    gen_pass(g.R, [&](int e, float v) {
+    gen_pass<NT>(g.R, [&](int e, float v) {
       const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
       if (ck < cm || ck < ckk) return;
       const int p = atomicAdd(&sh.ints[4], 1);
@@ -2352,7 +2365,7 @@ __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
         R.lds_bits = true;
       }
       // composites of the penalised row, zero-padded to n2, sorted descending (they are distinct)
-      gen_pass(R, [&](int e, float v) { xs[e] = comp(ord_key(v), static_cast<uint32_t>(e)); });
+      gen_pass<kGenThreads>(R, [&](int e, float v) { xs[e] = comp(ord_key(v), static_cast<uint32_t>(e)); });
       for (int i = V + tid; i < n2; i += kGenThreads) xs[i] = 0ull;
       __syncthreads();
       xsort(xs, n2, blk);
@@ -3980,16 +3993,25 @@ void launch_general_exact(const KArgs& a, int slots, hipStream_t st) {
   hipLaunchKernelGGL(k_general_exact, dim3(std::min(a.B, slots)), dim3(kGenThreads), dyn, st, a);
 }
 
-void launch_general(const KArgs& a, hipStream_t st) {
+void launch_general(const KArgs& a, int cus, hipStream_t st) {
   const size_t bytes = static_cast<size_t>(a.words) * sizeof(uint32_t);
-  const size_t dyn = (a.hist_off != nullptr && bytes <= kGenBitsLds) ? bytes : 0;
-  static bool configured = false;
-  if (!configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_general), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(kGenBitsLds));
-    configured = true;
-  }
-  hipLaunchKernelGGL(k_general, dim3(a.B), dim3(kGenThreads), dyn, st, a);
+  // the bitmap's LDS copy only where a row can be penalised
+  const bool none_pen = a.params == nullptr && a.shared.repeat == 1.0f;
+  const size_t dyn = (a.hist_off != nullptr && !none_pen && bytes <= kGenBitsLds) ? bytes : 0;
+  static std::once_flag configured;
+  std::call_once(configured, [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_general<1024>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGenBitsLds));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_general<512>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGenBitsLds));
+  });
+  // Two 512-thread workgroups per CU when every row is general (shared parameters), no LDS bitmap
+  // is needed (two workgroups' LDS then fit a CU) and the rows outnumber the CUs: wide, 512 x
+  // 151,936, 179 against 203 us. With fewer rows each keeps a CU of its own at 1024 threads.
+  if (cus > 0 && a.params == nullptr && dyn == 0 && a.B > cus)
+    hipLaunchKernelGGL(k_general<512>, dim3(a.B), dim3(512), 0, st, a);
+  else
+    hipLaunchKernelGGL(k_general<1024>, dim3(a.B), dim3(1024), dyn, st, a);
 }
 
 // ---- the scratch of vsmp_pick_batch_noalloc ---------------------------------------------------
