@@ -198,11 +198,13 @@ VSMP_API int vsmp_read_probe(vsmp_ctx* ctx, const void* p, long long bytes, void
  * Its accuracy against exp is what the tests bound. Returns 0 or -1. */
 VSMP_API int vsmp_exp_probe(vsmp_ctx* ctx, const double* x, double* y, long long n, void* stream);
 /* Diagnostics, no reference counterpart: y[i] = the numerator exp(double(d[i]) / temp) as the
- * general path's main pass takes it (a table over its level-0 buckets, scale qs = 4096 / span, the
- * span at most 64 temp), for d[i] = v - max <= 0 within the span, i < n (d: device floats, y:
- * device doubles). Its accuracy against exp is what the tests bound. Returns 0 or -1. */
+ * general path takes it over its level-0 buckets (scale qs = 4096 / span, the span at most 64 temp),
+ * for d[i] = v - max <= 0 within the span, i < n (d: device floats, y: device doubles): with
+ * fixed_point 0 the table numerator of its min-p statistics; otherwise the element's share of its
+ * bucket's mass (the table value times the element's fixed-point term). Its accuracy against exp
+ * is what the tests bound. Returns 0 or -1. */
 VSMP_API int vsmp_numer_probe(vsmp_ctx* ctx, const float* d, double* y, long long n, float temp, float qs,
-                              void* stream);
+                              int fixed_point, void* stream);
 
 /* A drop-in sampler object: verbo::Sampler (reference include/verbo/verbo.hpp:116-132) behind
  * a C handle, for FFI callers. Its history, xorshift stream and seeding are the reference's

@@ -382,6 +382,35 @@ def test_general_path_table_numerator_accuracy(ctx, span):
         assert abs(y[d == 0][0] - 1.0) <= 2.3e-16
 
 
+@pytest.mark.parametrize("span", [64.0, 20.0, 3.0, 1e-3])
+def test_general_path_fixed_point_mass_accuracy(ctx, span):
+    """Each element's share of its level-0 bucket's mass (the bucket pair's table value times the
+    element's fixed-point term, exp(x - c) rounded to 2^-40) against exp(d / temp) in long double:
+    within 5e-13 (relative; the 2^-40 rounding at most 4.6e-13 of it) plus |x| * 2^-52 for the
+    exponent's product form, over the same spans, temperatures and bucket edges as the table
+    numerators. Parity of the general path's top-p decisions leans on this bound: the near-tie band
+    (1e-11 and up) must exceed the prefixes' error, twice 5e-13 at most."""
+    import torch
+
+    rng = np.random.default_rng(37)
+    for temp in (1.0, 0.37, 1.9):
+        qs = np.float32(4096.0 / (span * temp))
+        edges = -(np.arange(4097, dtype=np.float64) / np.float64(qs))
+        d = np.concatenate([-np.float64(span * temp) * rng.random(400000), edges, np.nextafter(edges, 0.0),
+                            np.nextafter(edges, -np.inf), [0.0, -0.0]]).astype(np.float32)
+        d = d[(d <= 0) & (d >= -np.float32(span * temp) * np.float32(0.99999))]
+        y = ctx.numer_probe(torch.from_numpy(d).cuda(), temp, float(qs), fixed_point=True).cpu().numpy()
+        x = d.astype(np.longdouble) / np.longdouble(np.float32(temp))
+        ref = np.exp(x)
+        rel = np.abs(y.astype(np.longdouble) - ref) / ref
+        bound = 5e-13 + (np.abs(x) * np.longdouble(2.0**-52) if temp != 1.0 else 0.0)
+        excess = rel - bound
+        worst = int(np.argmax(excess))
+        assert excess[worst] <= 0, (span, temp, float(d[worst]), y[worst], float(ref[worst]), float(rel[worst]))
+        # the rounding is to nearest: the errors are not one-sided
+        assert (y > ref).any() and (y < ref).any()
+
+
 @pytest.mark.parametrize("dmode", ["split", "rows"])
 def test_greedy_split_parts(dmode):
     """Greedy batches cut into parts (one launch, the last part of a row writes its id) against the

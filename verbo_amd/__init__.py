@@ -137,7 +137,8 @@ def load_library():
         "vsmp_sampler_reset": (None, [_P]),
         "vsmp_read_probe": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P]),
         "vsmp_exp_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_longlong, _P]),
-        "vsmp_numer_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_longlong, ctypes.c_float, ctypes.c_float, _P]),
+        "vsmp_numer_probe": (ctypes.c_int, [_P, _P, _P, ctypes.c_longlong, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+                                            _P]),
         "vsmp_head_logits": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P, ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int, _P, ctypes.c_longlong, _P]),
         "vsmp_head_pick": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P, ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
@@ -380,9 +381,10 @@ class Context:
             raise _err()
         return y
 
-    def numer_probe(self, d, temp, qs, stream=None):
-        """vsmp_numer_probe: the main pass's numerators exp(double(d) / temp) for float32 device
-        tensor `d` (= v - max <= 0), buckets of scale qs; returns float64 y."""
+    def numer_probe(self, d, temp, qs, fixed_point=False, stream=None):
+        """vsmp_numer_probe: the general path's numerators exp(double(d) / temp) for float32 device
+        tensor `d` (= v - max <= 0), buckets of scale qs: the table numerators, or with fixed_point
+        each element's share of its bucket's mass; returns float64 y."""
         import torch
 
         if d.dtype != torch.float32 or not d.is_cuda:
@@ -391,7 +393,7 @@ class Context:
         y = torch.empty(d.shape, dtype=torch.float64, device=d.device)
         st = stream if stream is not None else torch.cuda.current_stream(d.device)
         if _lib.vsmp_numer_probe(self._h, d.data_ptr(), y.data_ptr(), d.numel(), float(temp), float(qs),
-                                 ctypes.c_void_p(st.cuda_stream)) != 0:
+                                 1 if fixed_point else 0, ctypes.c_void_p(st.cuda_stream)) != 0:
             raise _err()
         return y
 

@@ -835,13 +835,14 @@ int vsmp_exp_probe(vsmp_ctx* ctx, const double* x, double* y, long long n, void*
   return vsmp::hip_ok(hipGetLastError(), "exp-probe launch") ? 0 : -1;
 }
 
-int vsmp_numer_probe(vsmp_ctx* ctx, const float* d, double* y, long long n, float temp, float qs, void* stream) {
+int vsmp_numer_probe(vsmp_ctx* ctx, const float* d, double* y, long long n, float temp, float qs, int fixed_point,
+                     void* stream) {
   vsmp::clear_error();
   if (!ctx || (n > 0 && (!d || !y))) return vsmp::set_error("vsmp: null argument");
   if (n < 0 || !(temp > 0.0f) || !(qs >= 0.0f)) return vsmp::set_error("vsmp: numer probe needs n >= 0, temp > 0, qs >= 0");
   if (n == 0) return 0;
   if (!vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
-  vsmp::launch_numer_probe(d, y, n, temp, qs, static_cast<hipStream_t>(stream));
+  vsmp::launch_numer_probe(d, y, n, temp, qs, fixed_point != 0, static_cast<hipStream_t>(stream));
   return vsmp::hip_ok(hipGetLastError(), "numer-probe launch") ? 0 : -1;
 }
 

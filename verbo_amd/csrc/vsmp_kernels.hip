@@ -48,10 +48,9 @@ constexpr double kNearTopP = 1e-11;  // |acc - top_p| below this: reference roun
 // The general path's bound on that distance for a prefix of k numerators: its sums run in bucket
 // order, and a sum of k non-negative terms in any order lies within (k - 1) * 2^-53 of the exact
 // sum (relative), as does the reference's sequential one; the band is four times that, and never
-// below kNearTopP. The level-0 bucket masses round each term to 2^-41 of its value at most (fixed
-// point, numer_fix), which moves a prefix over the total by under 2^-40 = 9.1e-13: inside the band,
-// whose excess over 2 (k - 1) 2^-53 is at least 1e-11 - 2^-38 below k = 22,518 and 2 k 2^-53 >= 5e-12
-// above it.
+// below kNearTopP. The level-0 bucket masses hold each term within 5e-13 of its value (fixed point,
+// numer_fix), which moves a prefix over the total by under 1e-12: inside the band, whose excess
+// over 2 (k - 1) 2^-53 is at least 1e-11 - 2^-38 below k = 22,518 and 2 k 2^-53 >= 5e-12 above it.
 __device__ __forceinline__ double near_topp(int k) { return fmax(kNearTopP, 4.0 * static_cast<double>(k) * kTwoM53); }
 constexpr double kNearMinP = 1e-13;  // |pr - thr| / thr below this: exp last-bit territory
 constexpr double kNearDraw = 1e-6;   // draws this close to a CDF boundary are reported
@@ -1412,14 +1411,14 @@ __device__ __forceinline__ double numer_tab(const GenCtx& g, const double* etab,
 // The main pass's mass of an element of bucket q relative to its table point: exp(x - c_(q >> 1))
 // (within e^(+-1/64) of 1) as a fixed-point integer of 2^-40 units, rounded to nearest by one fma
 // (4097 + r s has a 2^-40 ulp; its low 52 bits are the value's). Bucket q's mass is then
-// etab[q >> 1] * sum * 2^-40: each term within 2^-41 (relative, times e^(1/64)) of numer_tab's, and
-// the sums exact and order-free (at most 2^20 terms of under 2^40.03 each).
+// etab[q >> 1] * sum * 2^-40: the sums exact and order-free (at most 2^20 terms of under 2^40.03
+// each), each term within 5e-13 (relative) of exp(x): 2^-41 e^(1/64) = 4.6e-13 of rounding, and
+// 2.1e-14 for the degree-5 Taylor polynomial of exp(r), |r| <= 1/64, that the rounding allows.
 __device__ __forceinline__ uint64_t numer_fix(const GenCtx& g, double w, float d, int q) {
   const double x = static_cast<double>(d) * g.inv_temp;
   const double r = fma(static_cast<double>(q | 1), w, x);
-  double s = fma(r, 0x1.6c16c16c16c17p-10, 0x1.1111111111111p-7);  // 1/720, 1/120
-  s = fma(r, s, 0x1.5555555555555p-5);                              // 1/24
-  s = fma(r, s, 0x1.5555555555555p-3);                              // 1/6
+  double s = fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);  // 1/120, 1/24
+  s = fma(r, s, 0x1.5555555555555p-3);                             // 1/6
   s = fma(r, s, 0.5);
   s = fma(r, s, 1.0);
   const double t = fma(r, s, 4097.0);
@@ -3546,10 +3545,11 @@ __global__ __launch_bounds__(256) void k_exp_probe(const double* __restrict__ x,
   for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) y[i] = exp_tab(x[i]);
 }
 
-// Diagnostics: y[i] = the main pass's numerator (numer_tab) of an element at d[i] = v - mx below the
-// row maximum, for buckets of scale qs and temperature temp, as the main pass places them.
+// Diagnostics: y[i] = the general path's numerator of an element at d[i] = v - mx below the row
+// maximum, for buckets of scale qs and temperature temp, as the main pass places them: the table
+// numerator (numer_tab), or with fixed_point the element's share of its bucket's mass (numer_fix).
 __global__ __launch_bounds__(256) void k_numer_probe(const float* __restrict__ d, double* __restrict__ y, long long n,
-                                                     float temp, float qs) {
+                                                     float temp, float qs, int fixed_point) {
   __shared__ double etab[kGenBuckets / 2];
   exp_tab_fill();
   __syncthreads();
@@ -3561,8 +3561,11 @@ __global__ __launch_bounds__(256) void k_numer_probe(const float* __restrict__ d
   for (int j = threadIdx.x; j < kGenBuckets / 2; j += 256) etab[j] = exp_tab(-static_cast<double>(2 * j + 1) * wq);
   __syncthreads();
   const long long stride = static_cast<long long>(gridDim.x) * 256;
-  for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
-    y[i] = numer_tab(g, etab, wq, d[i], max(q_of_d(g, d[i]), 0));  // d > 0 (no row holds one) kept in range
+  for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
+    const int q = max(q_of_d(g, d[i]), 0);  // d > 0 (no row holds one) kept in range
+    y[i] = fixed_point ? etab[q >> 1] * (static_cast<double>(numer_fix(g, wq, d[i], q)) * kFixUnit)
+                       : numer_tab(g, etab, wq, d[i], q);
+  }
 }
 
 // ---- the LM head's hand-off: bound and finish around k_head_gemm -------------------------------
@@ -3902,9 +3905,10 @@ __global__ __launch_bounds__(kHfNT) void k_head_finish(KArgs a, HeadArgs h) {
 
 }  // namespace
 
-void launch_numer_probe(const float* d, double* y, long long n, float temp, float qs, hipStream_t st) {
+void launch_numer_probe(const float* d, double* y, long long n, float temp, float qs, bool fixed_point, hipStream_t st) {
   const long long blocks = std::min<long long>((n + 255) / 256, 1024);
-  hipLaunchKernelGGL(k_numer_probe, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, d, y, n, temp, qs);
+  hipLaunchKernelGGL(k_numer_probe, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, d, y, n, temp, qs,
+                     fixed_point ? 1 : 0);
 }
 
 void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st) {
