@@ -269,6 +269,16 @@ def _general_batch(rng, kind, B=24, Vv=30000):
         p["temp"] = 0.25
         p["min_p"] = rng.choice([0.005, 0.008, 0.012], B)
         p["top_p"] = np.where(np.arange(B) % 2 == 0, 0.3, 0.995)
+    elif kind == "minp_overflow":  # capped rows whose tiny min-p threshold keeps some of the overflow
+        # bucket (64 to 69 temp below the maximum): the main pass cannot collect those, and a pass
+        # of its own collects the prefix
+        lg = np.full((B, Vv), -1e4)
+        for r in range(B):
+            lg[r, rng.integers(0, Vv, 300)] = rng.uniform(-66.0, -40.0, 300)
+            lg[r, rng.integers(0, Vv)] = 0.0
+        p["temp"] = 1.0
+        p["min_p"] = 1e-30
+        p["top_p"] = rng.choice([0.9, 1.0], B)
     elif kind == "cold":  # the buckets stop far short of the minimum: the overflow bucket holds most rows
         lg = rng.normal(0, 2.0, (B, Vv))
         p["temp"] = rng.choice([0.005, 0.02, 0.05], B)
@@ -285,9 +295,10 @@ def _general_batch(rng, kind, B=24, Vv=30000):
     return lg.astype(np.float32), p, h, off
 
 
-@pytest.mark.parametrize("kind", ["flat", "minp", "minp_large", "cold", "interleaved"])
+@pytest.mark.parametrize("kind", ["flat", "minp", "minp_large", "minp_overflow", "cold", "interleaved"])
 def test_general_path_pass_plans(ctx, mode, kind):
-    rng = np.random.default_rng({"flat": 11, "minp": 12, "minp_large": 15, "cold": 13, "interleaved": 14}[kind])
+    rng = np.random.default_rng({"flat": 11, "minp": 12, "minp_large": 15, "minp_overflow": 16, "cold": 13,
+                                 "interleaved": 14}[kind])
     lg, p, h, off = _general_batch(rng, kind)
     log("general pass plan", mode, kind)
     run = Run(ctx, lg, p, h, off)
@@ -296,7 +307,7 @@ def test_general_path_pass_plans(ctx, mode, kind):
     flags = run.info["flags"][gen]
     if kind == "flat":
         assert (flags & V.FLAG_ONE_PASS).mean() >= 0.5, flags
-    if kind == "minp":
+    if kind in ("minp", "minp_overflow"):
         assert (flags & V.FLAG_MINP_PREFIX).mean() >= 0.5, flags
     if kind == "minp_large":  # prefixes beyond the whole-prefix collection, both top-p outcomes
         keep_m, keep = run.info["keep_minp"][gen], run.info["keep"][gen]

@@ -1775,6 +1775,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   double* etab = sh.rmass;
   const double wq = table_width(g.qs, P.temp);
   for (int j = tid; j < kGenBuckets / 2; j += kGenThreads) etab[j] = exp_tab(-static_cast<double>(2 * j + 1) * wq);
+  // The main pass also collects the min-p prefix (its elements' exact numerators are taken there)
+  // into the list, which aliases the refinement counts, idle until the pass ends.
+  if (tid == 0) sh.ints[4] = 0;
   __syncthreads();
   const bool minp = P.min_p > 0.0f;
   const double thr = static_cast<double>(P.min_p);  // pr of the maximum is exactly 1
@@ -1796,7 +1799,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     auto excluded = [&](int e, float v) {
       return decltype(with_cut)::value && cut_k && comp(ord_key(v), static_cast<uint32_t>(e)) < g.ckk;
     };
-    auto add = [&](float v, float d, int q, uint64_t f) {
+    auto add = [&](int e, float v, float d, int q, uint64_t f) {
       if (decltype(ovf)::value && q == kGenBuckets - 1) {
         ++t_ocnt;
         if (capped) {
@@ -1819,6 +1822,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         if (p >= thr) {
           ++t_cntm;
           t_totm += p;
+          const int pos = atomicAdd(&sh.ints[4], 1);  // the min-p prefix, while it fits the list
+          if (pos < kGenCap) sh.list[pos] = comp(ord_key(v), static_cast<uint32_t>(e));
         }
       }
     };
@@ -1827,7 +1832,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         [&](int e, float v) {
           const float d = v - g.mx;
           const int q = q_of_d(g, d);
-          if (!excluded(e, v)) add(v, d, q, numer_fix(g, wq, d, q));
+          if (!excluded(e, v)) add(e, v, d, q, numer_fix(g, wq, d, q));
         },
         // the four masses first, then the four elements' histogram atomics together
         [&](int e, const float (&x)[4]) {
@@ -1842,7 +1847,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
           }
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            if (!excluded(e + c, x[c])) add(x[c], d[c], q[c], f[c]);
+            if (!excluded(e + c, x[c])) add(e + c, x[c], d[c], q[c], f[c]);
         });
   };
   // one instance per combination without a top-k restriction (the common case: no per-element
@@ -2025,23 +2030,30 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   Sel d;
   double target = 0.0;
   // Small min-p prefix: its elements (numerator >= thr, all of them close to the maximum) are
-  // collected whole in one pass, numerators taken only above a float floor below the cut; the
-  // top-p cut and the draw are then taken on the sorted prefix sums.
+  // collected whole, by the main pass as a rule; the top-p cut and the draw are then taken on the
+  // sorted prefix sums.
   if (minp && cntm >= 1u && cntm <= static_cast<uint32_t>(kGenCap)) {
-    const float vlo = g.mx + static_cast<float>(static_cast<double>(P.temp) * log(thr) * 1.001) - 1e-3f;
-    if (tid == 0) sh.ints[4] = 0;
+    // the main pass's list holds the prefix when every element it counted was collected there (not
+    // so for a capped row whose overflow bucket a tiny min-p threshold keeps); otherwise a pass
+    // collects every element above a float floor just below the min-p threshold
+    int m = sh.ints[4];
     __syncthreads();
-    gen_pass<NT>(g.R, [&](int e, float v) {
-      if (!(v >= vlo)) return;
-      if (!(numer_g(g, v) >= thr)) return;
-      const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
-      if (ck < g.ckk) return;
-      const int p = atomicAdd(&sh.ints[4], 1);
-      if (p < kGenCap) sh.list[p] = ck;
-    });
-    __syncthreads();
-    const int m = sh.ints[4];
-    __syncthreads();
+    if (m != static_cast<int>(cntm)) {
+      const float vlo = g.mx + static_cast<float>(static_cast<double>(P.temp) * log(thr) * 1.001) - 1e-3f;
+      if (tid == 0) sh.ints[4] = 0;
+      __syncthreads();
+      gen_pass<NT>(g.R, [&](int e, float v) {
+        if (!(v >= vlo)) return;
+        if (!(numer_g(g, v) >= thr)) return;
+        const uint64_t ck = comp(ord_key(v), static_cast<uint32_t>(e));
+        if (ck < g.ckk) return;
+        const int p = atomicAdd(&sh.ints[4], 1);
+        if (p < kGenCap) sh.list[p] = ck;
+      });
+      __syncthreads();
+      m = sh.ints[4];
+      __syncthreads();
+    }
     if (m == static_cast<int>(cntm)) {  // every kept element collected (else: the passes below)
       sort_desc(sh, sh.list, reinterpret_cast<uint64_t*>(sh.lpr), m);
       const Sel s = scan_sorted<true>(g, sh, sh.list, sh.lpr, m, 0, 0.0, topp ? tp * sum : INFINITY);
