@@ -95,7 +95,7 @@ def cpu_baseline(w, budget):
 
 
 def bench_single(args):
-    """The single-row decode workload as the survey states it: 10,000 consecutive draws on one fixed
+    """The single-row decode workload: 10,000 consecutive draws on one fixed
     1 x 49152 row and history (seed 42, no accept between draws). Reports microseconds per draw for
     the device-resident calls (value: draws/s), the same calls replayed from a HIP graph (100 per
     graph), the drop-in verbo::Sampler::pick on a host row (the path verbo's generate takes: the row

@@ -1,8 +1,8 @@
 """Records the golden output of verbo_generate on the reference's tiny test models, from the
 reference's own sampler (the unswapped build of tests/swap/build_swap.py), and copies those models
 into tests/golden/tiny/ as fixtures (they are data files the reference's own tests hold,
-tests/data/tiny-llama and tests/data/tiny-qwen2), so that the GPU box, which has no reference tree,
-can run the same scenarios through the swapped build.
+tests/data/tiny-llama and tests/data/tiny-qwen2), so that a machine without the reference tree can
+run the same scenarios through the swapped build.
 
     python tests/golden/make_capi_golden.py
 

@@ -1,10 +1,12 @@
-"""Builds verbo (the reference) with the MI355X sampler swapped in, as INTEGRATION.md documents it.
+"""Builds verbo (the reference) with the MI355X sampler swapped in by the two CMake blocks that the
+repository's integration notes give a maintainer (read from that file, so that the notes are what is
+built).
 
     python tests/swap/build_swap.py            # both builds and the drivers
     python tests/swap/build_swap.py swap       # the swapped build only
 
 - swap: a scratch copy of the reference tree (in a temporary directory outside this repository)
-  with the two CMake blocks of INTEGRATION.md applied, configured with -DVERBO_GPU_SAMPLER=ON and
+  with the two CMake blocks applied, configured with -DVERBO_GPU_SAMPLER=ON and
   -DVSMP_DIR=<this checkout>, built into tests/swap/_build/swap: libverbo.so, libverbo.a, the
   `verbo` CLI and `verbo_tests` (the reference's own test binary).
 - ref: the same tree without the blocks, built into tests/swap/_build/ref; its libverbo.so records
@@ -32,13 +34,13 @@ TARGETS = ["verbo", "verbo_shared", "verbo_cli", "verbo_tests"]
 
 
 def cmake_blocks(integration=ROOT / "INTEGRATION.md"):
-    """The two ```cmake blocks of INTEGRATION.md, (before add_library(verbo_obj), after the targets),
-    identified by their first comment line."""
+    """The two ```cmake blocks of the integration notes (before add_library(verbo_obj), after the
+    targets), identified by their first comment line."""
     blocks = re.findall(r"```cmake\n(.*?)```", integration.read_text(), re.S)
     before = [b for b in blocks if b.startswith("# vsmp: before add_library(verbo_obj")]
     after = [b for b in blocks if b.startswith("# vsmp: after the targets")]
     if len(before) != 1 or len(after) != 1:
-        raise RuntimeError("INTEGRATION.md must hold exactly one 'before' and one 'after' cmake block")
+        raise RuntimeError(f"{integration} must hold exactly one 'before' and one 'after' cmake block")
     return before[0], after[0]
 
 

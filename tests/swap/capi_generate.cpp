@@ -1,6 +1,6 @@
 // verbo_generate (reference src/capi.cpp:131-151) on the reference's tiny test models, through
 // whichever libverbo.so this program is linked with: the reference's own sampler, or the MI355X
-// sampler swapped in by the CMake blocks of INTEGRATION.md. Test infrastructure.
+// sampler swapped in by the integration notes' CMake blocks. Test infrastructure.
 //
 //   capi_generate <dir holding tiny-qwen2/ and tiny-llama/>
 //

@@ -1,9 +1,9 @@
-"""The reference-side swap of INTEGRATION.md, on the CPU: the two CMake blocks, taken from
-INTEGRATION.md itself, applied to a scratch copy of the reference tree, build every target
+"""The reference-side swap, on the CPU: the two CMake blocks, taken from the integration notes
+themselves, applied to a scratch copy of the reference tree, build every target
 (`verbo`, `libverbo.so`, the `verbo` CLI, `verbo_tests`); `libverbo.so` then needs `libvsmp.so`,
 leaves only those `verbo::Sampler` symbols undefined that `libvsmp.so` exports, and loads. The
 unswapped build reproduces the committed verbo_generate golden. Skipped without the reference
-tree (the GPU box has none)."""
+tree."""
 import ctypes
 import json
 import subprocess

@@ -1,4 +1,4 @@
-"""verbo with the MI355X sampler swapped in (INTEGRATION.md's CMake blocks; built by
+"""verbo with the MI355X sampler swapped in (the integration notes' CMake blocks; built by
 tests/swap/build_swap.py into tests/swap/_build/swap), run on the GPU:
 
 - verbo_generate (reference src/capi.cpp:131-151) through the swapped libverbo.so on the
