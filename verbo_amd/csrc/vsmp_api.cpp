@@ -42,7 +42,11 @@ namespace {
 template <class T>
 bool grow(T*& p, size_t& cap, size_t need, bool zero, const char* what, hipEvent_t done, hipStream_t zst = nullptr) {
   if (need <= cap && p) return true;
-  size_t n = std::max<size_t>(need, cap * 2);
+  // doubling spares small buffers repeated growth as a batch widens; a large one is sized to the
+  // request, so that what a call asks for bounds what the context holds
+  const size_t small = (size_t{64} << 20) / sizeof(T);  // elements below which a buffer grows by doubling
+  size_t n = need;
+  if (need < small) n = std::min(std::max(need, cap * 2), small);
   if (p) {
     if (!hip_ok(hipEventSynchronize(done), "wait for the last call before growing scratch")) return false;
     (void)hipFree(p);

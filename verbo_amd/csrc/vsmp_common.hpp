@@ -85,7 +85,8 @@ void launch_general_exact(const KArgs& a, int slots, hipStream_t st);
 void launch_numer_probe(const float* d, double* y, long long n, float temp, float qs, bool fixed_point, hipStream_t st);
 // Workgroups (and scratch slots of 2 * x_n entries) of k_general_exact for a batch of B rows: one
 // per row up to 256 (one per CU, so that a batch whose rows are all marked is redone in parallel),
-// at least 8, within 1 GB of slots (256 slots of 4 MB at 151,936 logits, 64 of 16 MB at 2^20).
+// at least 8, within 1 GB of slots (256 slots of 4 MB at 151,936 logits, 64 of 16 MB at 2^20); the
+// context sizes a scratch buffer this large to the request.
 inline int exact_slots(int x_n, int B) {
   const long long per = 16LL * x_n;
   const long long budget = (1LL << 30) / per;
