@@ -161,18 +161,21 @@ VSMP_API int vsmp_head_logits(vsmp_ctx* ctx, const void* hidden, long long ldh, 
                               void* stream);
 
 /* The LM head and the pick in one call: the ids vsmp_pick_batch would pick from the logits that
- * vsmp_head_logits writes, without writing them. Replaces Session's head product
- * (src/session.cpp:169) followed by Sampler::pick (src/sampler.cpp:50-109) on its row; the
- * reference has no such fused call. Greedy and small-k rows (temp <= 0, or 0 < top_k <= 256)
- * keep only the columns whose logit reaches a per-row bound (the k-th largest penalised logit of
- * the first 4096 columns) and never write their logits; other rows (top-k off or above 256) are
- * written whole and sampled by the general path.
+ * vsmp_head_logits writes. Replaces Session's head product (src/session.cpp:169) followed by
+ * Sampler::pick (src/sampler.cpp:50-109) on its row; the reference has no such fused call.
+ * Fused (batches of 16 to 64 rows, where it measured faster; any batch with
+ * VSMP_HEAD_ROUTE=fused set when the context is created): greedy and small-k rows (temp <= 0, or
+ * 0 < top_k <= 256) keep only the columns whose logit reaches a per-row bound (the k-th largest
+ * penalised logit of the first 4096 columns) and never write their logits; other rows (top-k off
+ * or above 256) are written whole and sampled by the general path. Other batches (or
+ * VSMP_HEAD_ROUTE=whole) write every row's logits and run the batched pick on them. Both routes
+ * give the same ids and diagnostics.
  *   hidden, head, B, V, D, ldh, ldw: as vsmp_head_logits.
  *   params ... dbg: as vsmp_pick_batch.
  *   logits/ldl: NULL, or a device fp32 [B][ldl] output that receives every row's logits too
  *       (16-byte aligned, ldl >= V and a multiple of 4).
- * Scratch (in the context): B x V candidate composites (8 bytes each), and B x V fp32 logits when
- * rows may take the general path and `logits` is NULL. Returns 0 or -1. */
+ * Scratch (in the context): fused, B x V candidate composites (8 bytes each); B x V fp32 logits
+ * when `logits` is NULL and the batch goes whole or may hold general rows. Returns 0 or -1. */
 VSMP_API int vsmp_head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head,
                             long long ldw, int B, int V, int D, const vsmp_params* params,
                             int params_per_row, const int* hist, const int* hist_off, int u_mode,

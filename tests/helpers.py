@@ -34,20 +34,25 @@ def log(*a):
 _CTX = {}
 
 
-def mode_ctx(mode=None):
-    """A context created under VSMP_MODE=mode (None: the planner's choice), cached per mode: the
+def mode_ctx(mode=None, head_route=None):
+    """A context created under VSMP_MODE=mode (None: the planner's choice) and
+    VSMP_HEAD_ROUTE=head_route (None: vsmp_head_pick's route by batch size), cached per pair: the
     library reads its tuning switches once, when a context is created."""
-    if mode not in _CTX:
-        old = os.environ.pop("VSMP_MODE", None)
+    key = (mode, head_route)
+    if key not in _CTX:
+        saved = {k: os.environ.pop(k, None) for k in ("VSMP_MODE", "VSMP_HEAD_ROUTE")}
         try:
             if mode:
                 os.environ["VSMP_MODE"] = mode
-            _CTX[mode] = V.Context(0)
+            if head_route:
+                os.environ["VSMP_HEAD_ROUTE"] = head_route
+            _CTX[key] = V.Context(0)
         finally:
-            os.environ.pop("VSMP_MODE", None)
-            if old is not None:
-                os.environ["VSMP_MODE"] = old
-    return _CTX[mode]
+            for k, v in saved.items():
+                os.environ.pop(k, None)
+                if v is not None:
+                    os.environ[k] = v
+    return _CTX[key]
 
 
 def csr(hists):

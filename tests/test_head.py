@@ -1,10 +1,11 @@
 """The LM head on the GPU and the pick fused into it (vsmp_head_logits, vsmp_head_pick).
 
 The head's product (reference src/session.cpp:169, matmul(m->head, ...)) is checked against a
-plain fp32 product of the same bf16 operands on the CPU. The fused pick is checked against the
-oracle (the reference's Sampler::pick, src/sampler.cpp:50-109) on the logits the head itself
-produces, with every comparison rule of the batched path (penalised ids, keep counts, candidate
-ids, sums, ids), and against vsmp_pick_batch on those logits, field for field.
+plain fp32 product of the same bf16 operands on the CPU. vsmp_head_pick is checked, on its route
+by batch size and with the fused route pinned for every batch, against the oracle (the reference's
+Sampler::pick, src/sampler.cpp:50-109) on the logits the head itself produces, with every
+comparison rule of the batched path (penalised ids, keep counts, candidate ids, sums, ids), and
+against vsmp_pick_batch on those logits, field for field.
 """
 import numpy as np
 import pytest
@@ -15,12 +16,14 @@ from helpers import Run, csr, log, mode_ctx
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture
-def ctx():
+@pytest.fixture(params=["auto", "fused"])
+def ctx(request):
+    """vsmp_head_pick's route by batch size (fused for 16 to 64 rows, the head's logits written and
+    the batched pick otherwise), and the fused route pinned for every batch."""
     import torch
 
     assert torch.cuda.is_available(), "the gpu tests need a ROCm device"
-    return mode_ctx(None)
+    return mode_ctx(None, None if request.param == "auto" else request.param)
 
 
 def bf16(a):

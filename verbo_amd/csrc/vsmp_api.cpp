@@ -77,8 +77,10 @@ struct vsmp_ctx {
   int device = 0;
   int cus = 256;                 // compute units of the device
   // tuning and testing switches, read from the environment when the context is created:
-  // VSMP_MODE=rows|slices|split (-1: the planner's choice), VSMP_SPLIT_P, VSMP_EPT
+  // VSMP_MODE=rows|slices|split (-1: the planner's choice), VSMP_SPLIT_P, VSMP_EPT,
+  // VSMP_HEAD_ROUTE=fused|whole (-1: vsmp_head_pick's route by batch size)
   int mode = -1;
+  int head_route = -1;  // 1: fused, 0: whole
   long long split_p = 0;
   int ept = 0;
   hipEvent_t done_ev = nullptr;  // recorded after the last work of every call (see grow)
@@ -548,25 +550,35 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
 
   hipEvent_t busy = ctx->done_ev;
   const bool shared_general = !params_per_row && path_host(*params, V, true) == kPathGeneral;
+  // The route. Fused, the call pays fixed stages (the probe's product, the bound, the finish: 25-31
+  // us at 151,936 x 896) against the logits it does not write and the sampler's read of them it
+  // saves; measured on MI355X (top-k 50, bf16 head of 151,936 x 896) that wins for batches of 16 to
+  // 64 rows (64 rows: 80.5 against 88.3 us; 16 rows: 71.3 against 73.0 us) and loses outside (1 row:
+  // 66.6 against 62.8 us, a tie at 12; 80 rows: 110.0 against 106.4 us; 256 rows: 157.4 against
+  // 150.0 us). Whole, the head's logits are written and the batched pick runs on them: the same ids
+  // and diagnostics, as the fused route is built to give.
+  constexpr int kHeadFuseMin = 16, kHeadFuseMax = 64;
+  const bool fused = ctx->head_route == 1 || (ctx->head_route < 0 && B >= kHeadFuseMin && B <= kHeadFuseMax);
+  const bool whole = shared_general || !fused;
   // logits written whole: the caller's, or (general rows possible, none kept by the caller) scratch
   float* full = logits;
   long long fld = ldl;
-  if (!full && (shared_general || params_per_row)) {
+  if (!full && (whole || params_per_row)) {
     fld = (static_cast<long long>(V) + 3) & ~3LL;
     if (!grow(ctx->h_full, ctx->n_full, static_cast<size_t>(B) * static_cast<size_t>(fld), false, "head scratch", busy))
       return -1;
     full = ctx->h_full;
   }
   HeadArgs h = head_args(hidden, ldh, head, ldw, B, V, D);
-  if (shared_general) {  // every row samples the whole row: the head, then the batched pick
+  if (whole) {  // the head, then the batched pick (every row of a shared general batch samples whole)
     h.col0 = 0;
     h.col1 = V;
     h.out = full;
     h.ldo = fld;
     launch_head_gemm(h, head_tile(B, false), st);
     if (!hip_ok(hipGetLastError(), "head launch")) return -1;
-    return launch_batch(ctx, full, B, V, fld, params, 0, hist, hist_off, u_mode, u, rng_state, counter, out, dbg, st,
-                        nullptr);
+    return launch_batch(ctx, full, B, V, fld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
+                        out, dbg, st, nullptr);
   }
   const int n0 = std::min(kHeadProbe, V);
   const int tile = head_tile(B, false);
@@ -702,6 +714,10 @@ vsmp_ctx* vsmp_ctx_new(int device) {
   c->device = dev;
   c->mode = vsmp::env_mode();
   if (const char* e = std::getenv("VSMP_SPLIT_P")) c->split_p = std::atoll(e);
+  if (const char* e = std::getenv("VSMP_HEAD_ROUTE")) {
+    if (std::strcmp(e, "fused") == 0) c->head_route = 1;
+    if (std::strcmp(e, "whole") == 0) c->head_route = 0;
+  }
   if (const char* e = std::getenv("VSMP_EPT")) {
     const int v = std::atoi(e);
     c->ept = (v == 16 || v == 32 || v == 64) ? v : 0;
