@@ -101,10 +101,9 @@ def head_run(ctx, hidden, head, params, hist=None, hist_off=None, cand_cap=128):
 
 
 def same_as_pick_batch(ctx, r, hist, hist_off):
-    """The fused run's ids and row diagnostics equal vsmp_pick_batch's on the same logits. The
-    general path's sums (top-k off or above 256: the same kernel on both sides) accumulate a mass
-    histogram with LDS atomics, so they agree to 1e-12 rather than to the bit; every other field,
-    and every field of greedy and small-k rows, to the bit."""
+    """The head pick's ids and row diagnostics equal vsmp_pick_batch's on the same logits: the
+    general path's fp64 sums (top-k off or above 256) to 1e-12, every other field, and every field
+    of greedy and small-k rows, to the bit."""
     b = Run(ctx, r.logits, r.params, hist, hist_off, u=r.u, cand_cap=r.cand_cap)
     assert np.array_equal(r.ids, b.ids)
     for f in ("id", "path", "k", "keep_minp", "keep", "rank", "last_id", "n_pen", "mx", "u"):
@@ -265,3 +264,35 @@ def test_head_pick_row_tiles_padding_and_draw_modes(ctx):
     b = ctx.pick_batch(logits, per_row, dh, dho, V.U_COUNTER, counter=5)
     torch.cuda.synchronize()
     assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
+
+
+def test_head_pick_routes_agree():
+    """VSMP_HEAD_ROUTE pins vsmp_head_pick's route. At 32 rows (fused by batch size) the whole route
+    (the head's logits written, then the batched pick) and the fused one give the same ids, the
+    same row diagnostics and the same candidate ids, for greedy, small-k and general parameters
+    with penalised histories and counter draws."""
+    import torch
+
+    B, Vv, D = 32, 20000, 128
+    hidden, head = operands(41, B, Vv, D)
+    rng = np.random.default_rng(41)
+    h, off = csr([list(rng.integers(0, Vv, 200)) for _ in range(B)])
+    hist = torch.from_numpy(h).cuda()
+    hoff = torch.from_numpy(off).cuda()
+    for prm in (V.Params(temp=0.0, repeat=1.2, repeat_last=0), V.Params(temp=0.8, top_k=50, top_p=0.95,
+                min_p=0.05, repeat=1.1, repeat_last=0, seed=5), V.Params(temp=1.0, top_k=0, top_p=0.9, repeat=1.1,
+                repeat_last=64, seed=6)):
+        got = {}
+        for route in ("fused", "whole"):
+            c = mode_ctx(None, route)
+            info = torch.zeros(B * 72, dtype=torch.uint8, device="cuda")
+            cand = torch.full((B, 64), -1, dtype=torch.int32, device="cuda")
+            out = c.head_pick(hidden, head, prm, hist, hoff, V.U_COUNTER, counter=3, info=info, cand_ids=cand)
+            torch.cuda.synchronize()
+            got[route] = (out.cpu().numpy(), V.row_info(info), cand.cpu().numpy())
+        (fo, fi, fc), (wo, wi, wc) = got["fused"], got["whole"]
+        assert np.array_equal(fo, wo), prm
+        for f in ("id", "path", "k", "keep_minp", "keep", "rank", "last_id", "n_pen", "mx", "u"):
+            assert np.array_equal(fi[f], wi[f]), (prm, f)
+        assert np.allclose(fi["sum"], wi["sum"], rtol=1e-12, atol=0) and np.allclose(fi["tot"], wi["tot"], rtol=1e-12, atol=0)
+        assert np.array_equal(fc, wc), prm
