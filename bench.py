@@ -439,15 +439,25 @@ def main():
         print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "us_per_copy": ms_per_step * 1e3,
                           "GB_per_s_read_plus_write": gbs}), flush=True)
         return
-    # attainable read bandwidth on this box: the library's plain streaming-read kernel over the same buffers
+    # attainable read bandwidth on this box: the library's plain streaming-read kernel over the same
+    # buffers, from a graph as the steps are (issued one by one from Python, the reads would wait on
+    # the host's launch rate: each takes about 23 us on the GPU)
     for i in range(nbuf):
         ctx.read_probe(bufs[i], stream=stream)
     torch.cuda.synchronize()
     r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = 4 * nbuf
+    reps = 8 * nbuf
+    rgraph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(stream)
+    with torch.cuda.graph(rgraph, stream=cap):
+        for i in range(reps):
+            ctx.read_probe(bufs[i % nbuf], stream=cap)
+    torch.cuda.synchronize()
+    rgraph.replay()
+    settle(rgraph, stream)
     r0.record(stream)
-    for i in range(reps):
-        ctx.read_probe(bufs[i % nbuf], stream=stream)
+    rgraph.replay()
     r1.record(stream)
     torch.cuda.synchronize()
     attainable = reps * nbytes / (r0.elapsed_time(r1) * 1e-3) / 1e9
