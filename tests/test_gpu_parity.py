@@ -343,6 +343,37 @@ def test_general_path_top_p_ties_exact(ctx, mode):
                 assert int(g["flags"]) & V.FLAG_SEQ_CUTS, (Vv, r, int(g["flags"]))
 
 
+def test_general_path_top_p_ties_sorted(ctx, mode):
+    """Near-tie rows that are not flat, so that the exact redo sorts them: a multiple of four
+    logits at 0 at random positions, the rest at -1000 (numerators exp(-1000) = 0 in fp64), so the
+    top-p running sum meets top_p at rounding distance inside the zeros, which the sort must put
+    first in index order. Half the rows carry a penalised history (the penalty takes -1000 to -1200
+    and leaves 0). Keep counts and ids equal the oracle's, and rows at a tie carry
+    VSMP_FLAG_SEQ_CUTS."""
+    rng = np.random.default_rng(62)
+    for Vv in (4098, 49152, 151936):
+        B = 4
+        lg = np.full((B, Vv), -1000.0, np.float32)
+        n0 = 4 * (Vv // 10)
+        for r in range(B):
+            lg[r, rng.choice(Vv, n0, replace=False)] = 0.0
+        p = V.params_array(n=B, temp=1.0, top_k=0, top_p=0.5, min_p=0.0, repeat=1.0, repeat_last=0, seed=7)
+        p["top_p"] = [0.5, 0.25, 0.75, 0.5]
+        p["repeat"] = [1.0, 1.2, 1.0, 1.2]
+        p["seed"] = rng.integers(1, 1 << 62, B)
+        h, off = csr([list(rng.integers(0, Vv, 100)) if r % 2 else [] for r in range(B)])
+        log("top-p ties, sorted redo", mode, Vv)
+        run = Run(ctx, lg, p, h, off, cand_cap=128)
+        run.report()
+        for r in range(B):
+            o, g = run.o_info[r], run.info[r]
+            assert int(g["keep"]) == int(o["keep"]), (Vv, r, int(g["keep"]), int(o["keep"]))
+            assert run.ids[r] == run.o_ids[r], (Vv, r, run.ids[r], run.o_ids[r])
+            if o["topp_margin"] < 1e-11:
+                assert int(g["flags"]) & V.FLAG_SEQ_CUTS, (Vv, r, int(g["flags"]))
+        assert (run.info["flags"] & V.FLAG_SEQ_CUTS).any()
+
+
 def test_general_path_exp_accuracy(ctx):
     """The general path's fp64 exp (a 64-entry table method) against exp in long double: within
     1.01 ulp over [-745, 0] (the reference's libm exp is within one ulp too), exactly 1 at 0 and 0

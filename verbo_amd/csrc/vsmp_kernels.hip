@@ -2324,12 +2324,114 @@ __device__ void lds_serial(const double* v, int n, double x0, F f, Op op, Stop s
   }
 }
 
+// src/sampler.cpp:92-100 on a row whose numerators all equal 1: acc += q (q = 1 / sum, the IEEE
+// quotient) in order over [0, n); the first i whose acc >= tp, n when none. A running sum of
+// positive terms never decreases, so eight additions are taken before one test.
+__device__ __forceinline__ int flat_topp(double q, double tp, int n) {
+  double acc = 0.0;
+  int i = 0;
+  for (; i + 8 <= n; i += 8) {
+    double t[8];
+    double x = acc;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      x += q;
+      t[j] = x;
+    }
+    if (t[7] >= tp) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (t[j] >= tp) return i + j;
+    }
+    acc = x;
+  }
+  for (; i < n; ++i) {
+    acc += q;
+    if (acc >= tp) return i;
+  }
+  return n;
+}
+
+// The exact redo of a flat row: every penalised value equal (key_val of one order key) and
+// exp(0) = 1 its every numerator. The reference's sort leaves the row in index order
+// (src/sampler.cpp:72-78), so its top-k prefix is [0, k); the sums of :84 and :101 add ones, so
+// they are the counts k and keep, exactly; min-p (:86-91) keeps one element when 1 < min_p and all
+// k otherwise. The top-p sum runs in order (flat_topp). The draw's remainders r_i = r_(i-1) - 1
+// from r_(-1) = u * tot are exact while r_(i-1) >= 1 (a multiple of its ulp <= 1, less one, stays
+// representable), so the first i with r_i <= 0 is ceil(r0) - 1 when r0 > 1, else 0, and the last
+// two remainders are r0 - i and that less one. Thread 0 writes what the general redo writes.
+__device__ void exact_flat_row(const KArgs& a, int row, const vsmp_params& P, int V) {
+  __shared__ int fkeep;
+  const int k = top_k_of(P, V);
+  if (threadIdx.x == 0) {
+    const double sum = static_cast<double>(k);
+    int keep = k;
+    if (P.min_p > 0.0f && k > 1 && !(1.0 >= static_cast<double>(P.min_p))) keep = 1;
+    const int keep_minp = keep;
+    if (P.top_p > 0.0f && P.top_p < 1.0f) {
+      const int i = flat_topp(1.0 / sum, static_cast<double>(P.top_p), keep);
+      if (i + 1 < keep) keep = i + 1;
+    }
+    const double tot = static_cast<double>(keep);
+    const double r0 = a.x_u[row] * tot;
+    int pick;
+    bool picked = true;
+    double rl, rb;  // the last remainder taken and the one before it
+    if (!(r0 > 1.0)) {
+      pick = 0;
+      rb = r0;
+      rl = r0 - 1.0;
+    } else {
+      const double c = ceil(r0);
+      const int j = static_cast<int>(c) - 1;
+      if (j < keep) {
+        pick = j;
+        rb = r0 - static_cast<double>(j);
+        rl = rb - 1.0;
+      } else {
+        picked = false;
+        pick = keep - 1;
+        rl = r0 - static_cast<double>(keep);
+        rb = keep >= 2 ? r0 - static_cast<double>(keep - 1) : r0;
+      }
+    }
+    double mg = fabs(rl);
+    if (picked && pick > 0 && rb < mg) mg = rb;
+    a.out[row] = pick;
+    if (a.info) {
+      vsmp_row_info inf = a.info[row];
+      inf.id = pick;
+      inf.keep_minp = keep_minp;
+      inf.keep = keep;
+      inf.rank = pick;
+      inf.last_id = keep - 1;
+      inf.sum = sum;
+      inf.tot = tot;
+      inf.draw_margin = tot > 0.0 ? mg / tot : 0.0;
+      inf.flags = (inf.flags & ~VSMP_FLAG_DRAW_NEAR) | VSMP_FLAG_SEQ_CUTS |
+                  (inf.draw_margin < kNearDraw ? VSMP_FLAG_DRAW_NEAR : 0);
+      a.info[row] = inf;
+    }
+    fkeep = keep;
+  }
+  __syncthreads();
+  if (a.cand_ids && a.cand_cap > 0) {  // diagnostics: the redone draw set replaces k_general's
+    const int m = min(fkeep, a.cand_cap);
+    for (int j = threadIdx.x; j < m; j += kGenThreads) {
+      const size_t o = static_cast<size_t>(row) * a.cand_cap + j;
+      a.cand_ids[o] = j;
+      if (a.cand_pr) a.cand_pr[o] = 1.0;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
   __shared__ int list[kGenThreads];
   __shared__ int nlist;
   __shared__ int xkeep;
   __shared__ double xd[8];
   __shared__ int xi[4];
+  __shared__ uint32_t xk[2];  // the row's smallest and largest penalised order key
   __shared__ __align__(16) uint64_t blk[kXBlock];  // sort blocks; staged chunks of the chains
   double* stage = reinterpret_cast<double*>(blk);
   const int tid = threadIdx.x;
@@ -2374,6 +2476,36 @@ __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
         __syncthreads();
         R.bits = lb;
         R.lds_bits = true;
+      }
+      // A flat row (every penalised value the same, as in a padding row) is decided without the
+      // sort: its order is the index order and each numerator is exactly 1.
+      {
+        if (tid == 0) {
+          xk[0] = 0xFFFFFFFFu;
+          xk[1] = 0u;
+        }
+        __syncthreads();
+        uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+        gen_pass<kGenThreads>(R, [&](int, float v) {
+          const uint32_t kk = ord_key(v);
+          kmin = min(kmin, kk);
+          kmax = max(kmax, kk);
+        });
+        for (int o = 32; o > 0; o >>= 1) {
+          kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmin), o)));
+          kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), o)));
+        }
+        if ((tid & 63) == 0) {
+          atomicMin(&xk[0], kmin);
+          atomicMax(&xk[1], kmax);
+        }
+        __syncthreads();
+      }
+      const float fv = key_val(xk[1]);
+      if (xk[0] == xk[1] && numer(fv, fv, P.temp) == 1.0) {
+        exact_flat_row(a, row, P, V);
+        __syncthreads();  // the bitmap is reused by the next row
+        continue;
       }
       // composites of the penalised row, zero-padded to n2, sorted descending (they are distinct)
       gen_pass<kGenThreads>(R, [&](int e, float v) { xs[e] = comp(ord_key(v), static_cast<uint32_t>(e)); });
