@@ -9,7 +9,9 @@ replicated into enough buffers (> 600 MB) that consecutive steps never find thei
 256 MB Infinity Cache. Prints one JSON line (stdout); progress goes to stderr.
 
 Fields: value = rows/s over the timed steps; roofline.achieved = algorithmic bytes per call /
-mean call duration (two HIP events around the timed steps, on the launch stream); cpu_baseline = the reference sampler
+mean call duration (two HIP events around the timed steps, on the launch stream);
+config.replays_ms_per_step = the median, least and greatest per-step time over 20 further replays
+of the same graph, each between its own events (the run-to-run spread); cpu_baseline = the reference sampler
 compiled from its sources (oracle/_ref), or the oracle restatement when that is not built, timed
 on this host for a bounded sample of the same rows: one thread (value, cores) and every host
 thread (value_all_cores, cores_all).
@@ -433,6 +435,16 @@ def main():
         e1.record(stream)
         torch.cuda.synchronize()
         eager_ms = e0.elapsed_time(e1) / args.steps
+    # run-to-run spread: 20 more replays of the same graph, each between its own two events
+    reps_ms = []
+    if use_graph:
+        for _ in range(20):
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            reps_ms.append(e0.elapsed_time(e1) / args.steps)
+        reps_ms.sort()
     log(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (wall {wall * 1e3:.2f} ms)")
     if args.copy:
         gbs = 2 * nbytes / (ms_per_step * 1e-3) / 1e9
@@ -481,7 +493,9 @@ def main():
         "config": {"workload": DESCR[args.workload], "B": w.B, "V": w.V, "buffers": nbuf,
                    "algorithmic_bytes_per_step": alg, "epilogue_dtype": "f64",
                    "issue": "hip_graph" if use_graph else "eager",
-                   "eager_ms_per_step": eager_ms},
+                   "eager_ms_per_step": eager_ms,
+                   "replays_ms_per_step": {"n": len(reps_ms), "median": reps_ms[len(reps_ms) // 2],
+                                           "min": reps_ms[0], "max": reps_ms[-1]} if reps_ms else None},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "attainable_read": attainable},
     }
