@@ -185,8 +185,9 @@ VSMP_API int vsmp_head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, co
 
 /* One pick on a HOST logits row with a host history and a supplied draw u: the computation of
  * verbo::Sampler::pick(logits, n) (reference src/sampler.cpp:50-109) for a sampler whose history
- * is hist[0..H) and whose next stream draw is u. Copies the row to the device, runs the kernels
- * on the context's stream and waits. Writes the id to *out_id (and *info if not NULL).
+ * is hist[0..H) and whose next stream draw is u. Writes the row, history and draw into a pinned
+ * host area of the context that the device reads through its mapping (no copies), runs the
+ * kernels on the context's stream and waits. Writes the id to *out_id (and *info if not NULL).
  * Returns 0, or -1 (n <= 0, bad arguments, HIP error). */
 VSMP_API int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params* params,
                             const int* hist, int H, double u, int* out_id, vsmp_row_info* info);
