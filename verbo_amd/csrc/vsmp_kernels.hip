@@ -31,7 +31,9 @@
 //  k_exp_probe   the general path's fp64 exp over an array, for measuring its accuracy.
 //  k_numer_probe the main pass's table numerators over an array, for measuring their accuracy.
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
+#include <initializer_list>
 #include <mutex>
 #include <type_traits>
 
@@ -4098,6 +4100,24 @@ void launch_stage1(const KArgs& a, int ept, int grid, hipStream_t st) {
   }
 }
 
+// Raises the dynamic LDS limit of kernels above the default, once per device: the attribute
+// belongs to each device's instance of a kernel, so a process that launches on several devices
+// sets it on each (devices 64 and up are set at every launch).
+struct DynLdsOnce {
+  std::atomic<unsigned long long> done{0};
+  std::mutex m;
+};
+static void allow_dyn_lds(DynLdsOnce& o, std::initializer_list<const void*> fns, int bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  const unsigned long long bit = (dev >= 0 && dev < 64) ? 1ull << dev : 0ull;
+  if (bit && (o.done.load(std::memory_order_acquire) & bit)) return;
+  std::lock_guard<std::mutex> g(o.m);
+  if (bit && (o.done.load(std::memory_order_relaxed) & bit)) return;
+  for (const void* fn : fns) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  o.done.fetch_or(bit, std::memory_order_release);
+}
+
 void launch_head_bound(const KArgs& a, const HeadArgs& h, const float* probe, long long pld, int n0, int write_all,
                        uint8_t* rmode, uint32_t* tk, hipStream_t st) {
   hipLaunchKernelGGL(k_head_bound, dim3(a.B), dim3(kHbNT), 0, st, a, h, probe, pld, n0, write_all, rmode, tk);
@@ -4105,12 +4125,8 @@ void launch_head_bound(const KArgs& a, const HeadArgs& h, const float* probe, lo
 
 void launch_head_finish(const KArgs& a, const HeadArgs& h, hipStream_t st) {
   const size_t dyn = static_cast<size_t>((a.V + 31) / 32) * sizeof(uint32_t);
-  static bool configured = false;
-  if (!configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_head_finish), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(kRowMaxDynLds));
-    configured = true;
-  }
+  static DynLdsOnce configured;
+  allow_dyn_lds(configured, {reinterpret_cast<const void*>(k_head_finish)}, static_cast<int>(kRowMaxDynLds));
   hipLaunchKernelGGL(k_head_finish, dim3(a.B), dim3(kHfNT), dyn, st, a, h);
 }
 
@@ -4120,24 +4136,16 @@ void launch_finish(const KArgs& a, hipStream_t st) {
 
 void launch_rows(const KArgs& a, hipStream_t st) {
   const size_t dyn = static_cast<size_t>((a.V + 31) / 32) * sizeof(uint32_t);
-  static bool configured = false;
-  if (!configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_rows), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(kRowMaxDynLds));
-    configured = true;
-  }
+  static DynLdsOnce configured;
+  allow_dyn_lds(configured, {reinterpret_cast<const void*>(k_rows)}, static_cast<int>(kRowMaxDynLds));
   hipLaunchKernelGGL(k_rows, dim3(a.B), dim3(kRowNT), dyn, st, a);
 }
 
 void launch_general_exact(const KArgs& a, int slots, hipStream_t st) {
   const size_t bytes = static_cast<size_t>(a.words) * sizeof(uint32_t);
   const size_t dyn = (a.hist_off != nullptr && a.gen_fused && bytes <= kGenBitsLds) ? bytes : 0;
-  static bool configured = false;
-  if (!configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_general_exact),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGenBitsLds));
-    configured = true;
-  }
+  static DynLdsOnce configured;
+  allow_dyn_lds(configured, {reinterpret_cast<const void*>(k_general_exact)}, static_cast<int>(kGenBitsLds));
   hipLaunchKernelGGL(k_general_exact, dim3(std::min(a.B, slots)), dim3(kGenThreads), dyn, st, a);
 }
 
@@ -4146,13 +4154,10 @@ void launch_general(const KArgs& a, int cus, hipStream_t st) {
   // the bitmap's LDS copy only where a row can be penalised
   const bool none_pen = a.params == nullptr && a.shared.repeat == 1.0f;
   const size_t dyn = (a.hist_off != nullptr && !none_pen && bytes <= kGenBitsLds) ? bytes : 0;
-  static std::once_flag configured;
-  std::call_once(configured, [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_general<1024>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGenBitsLds));
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_general<512>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGenBitsLds));
-  });
+  static DynLdsOnce configured;
+  allow_dyn_lds(configured,
+                {reinterpret_cast<const void*>(k_general<1024>), reinterpret_cast<const void*>(k_general<512>)},
+                static_cast<int>(kGenBitsLds));
   // Two 512-thread workgroups per CU when every row is general (shared parameters), no LDS bitmap
   // is needed (two workgroups' LDS then fit a CU) and the rows outnumber the CUs: wide, 512 x
   // 151,936, 179 against 203 us. With fewer rows each keeps a CU of its own at 1024 threads.
