@@ -62,7 +62,7 @@ struct vsmp_dsampler {
 namespace {
 
 bool ds_free_bufs(vsmp_dsampler* s) {
-  (void)hipSetDevice(s->device);
+  vsmp::DeviceScope scope(s->device);
   for (void* p : {static_cast<void*>(s->hist), static_cast<void*>(s->meta), static_cast<void*>(s->rng),
                   static_cast<void*>(s->out)})
     if (p) (void)hipFree(p);
@@ -115,7 +115,12 @@ vsmp_dsampler* vsmp_dsampler_new(int device, const vsmp_params* cfg) {
     delete s;
     return nullptr;
   }
-  (void)hipGetDevice(&s->device);
+  s->device = vsmp::ctx_device(s->ctx);
+  vsmp::DeviceScope scope(s->device);  // the sampler's buffers live on the context's device
+  if (!scope.ok()) {
+    vsmp_dsampler_free(s);
+    return nullptr;
+  }
   s->cfg = *cfg;
   void* host = nullptr;
   const int first_cap = cfg->repeat_last > 0 ? 4 * cfg->repeat_last : 256;
@@ -140,7 +145,8 @@ void vsmp_dsampler_free(vsmp_dsampler* s) {
 int vsmp_dsampler_reset(vsmp_dsampler* s) {
   vsmp::clear_error();
   if (!s) return vsmp::set_error("vsmp: null sampler");
-  if (!hip_ok(hipSetDevice(s->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok()) return -1;
   std::uint64_t st[2];
   vsmp::seed_stream(s->cfg.seed, st);
   if (!hip_ok(hipMemcpy(s->rng, st, sizeof st, hipMemcpyHostToDevice), "copy draw stream")) return -1;
@@ -151,7 +157,8 @@ int vsmp_dsampler_accept(vsmp_dsampler* s, const int* ids, int n, void* stream) 
   vsmp::clear_error();
   if (!s || (n > 0 && !ids) || n < 0) return vsmp::set_error("vsmp: bad accept arguments");
   if (n == 0) return 0;
-  if (!hip_ok(hipSetDevice(s->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok()) return -1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int rl = s->cfg.repeat_last;
   const int len = accepted_length(s->h, n, rl);
@@ -179,7 +186,8 @@ int vsmp_dsampler_pick_async(vsmp_dsampler* s, const float* logits, int n, int* 
   vsmp::clear_error();
   if (!s) return vsmp::set_error("vsmp: null sampler");
   if (n <= 0) return vsmp::set_error("vsmp: pick needs at least one logit");
-  if (!hip_ok(hipSetDevice(s->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok()) return -1;
   const long long ld = (static_cast<long long>(n) + 3) & ~3LL;
   return vsmp::pick_batch(s->ctx, logits, 1, n, ld, &s->cfg, 0, s->hist, s->meta, VSMP_U_XORSHIFT, nullptr, s->rng, 0,
                           out ? out : s->out, nullptr, static_cast<hipStream_t>(stream));
@@ -235,7 +243,12 @@ vsmp_bsampler* vsmp_bsampler_new(int device, int n, const vsmp_params* params, i
     delete s;
     return nullptr;
   }
-  (void)hipGetDevice(&s->device);
+  s->device = vsmp::ctx_device(s->ctx);
+  vsmp::DeviceScope scope(s->device);  // the sampler's buffers live on the context's device
+  if (!scope.ok()) {
+    vsmp_bsampler_free(s);
+    return nullptr;
+  }
   s->n = n;
   s->cap = cap;
   std::vector<std::uint64_t> st(2 * static_cast<size_t>(n));
@@ -268,7 +281,7 @@ vsmp_bsampler* vsmp_bsampler_new(int device, int n, const vsmp_params* params, i
 void vsmp_bsampler_free(vsmp_bsampler* s) {
   if (!s) return;
   if (s->ctx) vsmp_ctx_free(s->ctx);
-  (void)hipSetDevice(s->device);
+  vsmp::DeviceScope scope(s->device);
   for (void* p : {static_cast<void*>(s->params), static_cast<void*>(s->rng), static_cast<void*>(s->hist),
                   static_cast<void*>(s->off), static_cast<void*>(s->len), static_cast<void*>(s->full)})
     if (p) (void)hipFree(p);
@@ -280,7 +293,8 @@ int vsmp_bsampler_accept_host(vsmp_bsampler* s, int row, const int* ids, int m) 
   vsmp::clear_error();
   if (!s || row < 0 || row >= s->n || m < 0 || (m > 0 && !ids)) return vsmp::set_error("vsmp: bad accept arguments");
   if (m == 0) return 0;
-  if (!hip_ok(hipSetDevice(s->device), "hipSetDevice") || !hip_ok(hipDeviceSynchronize(), "synchronise")) return -1;
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok() || !hip_ok(hipDeviceSynchronize(), "synchronise")) return -1;
   // the row's parameters and current length, from the device (prompts are accepted before decoding)
   vsmp_params p{};
   int h = 0;
@@ -308,7 +322,8 @@ int vsmp_bsampler_accept_host(vsmp_bsampler* s, int row, const int* ids, int m) 
 int vsmp_bsampler_pick(vsmp_bsampler* s, const float* logits, int V, long long ld, int* out, void* stream) {
   vsmp::clear_error();
   if (!s) return vsmp::set_error("vsmp: null sampler");
-  if (!hip_ok(hipSetDevice(s->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok()) return -1;
   return vsmp::pick_batch(s->ctx, logits, s->n, V, ld, s->params, 1, s->hist, s->off, VSMP_U_XORSHIFT, nullptr, s->rng, 0,
                           out, nullptr, static_cast<hipStream_t>(stream), s->len);
 }
@@ -316,7 +331,8 @@ int vsmp_bsampler_pick(vsmp_bsampler* s, const float* logits, int V, long long l
 int vsmp_bsampler_accept(vsmp_bsampler* s, const int* ids, const int* active, void* stream) {
   vsmp::clear_error();
   if (!s || !ids) return vsmp::set_error("vsmp: bad accept arguments");
-  if (!hip_ok(hipSetDevice(s->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok()) return -1;
   vsmp::launch_hist_accept(s->hist, s->off, s->len, s->cap, s->params, vsmp_params{}, ids, 0, active, s->n, s->full,
                            static_cast<hipStream_t>(stream));
   return hip_ok(hipGetLastError(), "accept launch") ? 0 : -1;
@@ -325,7 +341,8 @@ int vsmp_bsampler_accept(vsmp_bsampler* s, const int* ids, const int* active, vo
 int vsmp_bsampler_full(vsmp_bsampler* s, void* stream) {
   vsmp::clear_error();
   if (!s) return vsmp::set_error("vsmp: null sampler");
-  if (!hip_ok(hipSetDevice(s->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok()) return -1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (!hip_ok(hipMemcpyAsync(s->host, s->full, sizeof(int), hipMemcpyDeviceToHost, st), "copy flag") ||
       !hip_ok(hipStreamSynchronize(st), "synchronise"))

@@ -9,6 +9,7 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "verbo/verbo.hpp"
 #include "vsmp.h"
@@ -42,10 +43,15 @@ struct CtxDeleter {
   void operator()(vsmp_ctx* c) const { vsmp_ctx_free(c); }
 };
 
+// The calling thread's context on its current HIP device, created there on first use.
 vsmp_ctx* thread_ctx() {
-  thread_local std::unique_ptr<vsmp_ctx, CtxDeleter> ctx;
+  thread_local std::vector<std::unique_ptr<vsmp_ctx, CtxDeleter>> ctxs;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) throw std::runtime_error("vsmp: no current HIP device");
+  if (ctxs.size() <= static_cast<size_t>(dev)) ctxs.resize(static_cast<size_t>(dev) + 1);
+  auto& ctx = ctxs[static_cast<size_t>(dev)];
   if (!ctx) {
-    ctx.reset(vsmp_ctx_new(-1));
+    ctx.reset(vsmp_ctx_new(dev));
     if (!ctx) throw std::runtime_error(vsmp_last_error());
   }
   return ctx.get();

@@ -693,6 +693,10 @@ int pick_batch_noalloc(const float* logits, int B, int V, long long ld, const vs
 }  // namespace
 }  // namespace vsmp
 
+namespace vsmp {
+int ctx_device(const vsmp_ctx* c) { return c->device; }
+}  // namespace vsmp
+
 extern "C" {
 
 const char* vsmp_last_error(void) { return vsmp::g_err.c_str(); }
@@ -703,7 +707,8 @@ vsmp_ctx* vsmp_ctx_new(int device) {
   vsmp::clear_error();
   int dev = device;
   if (dev < 0 && !vsmp::hip_ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
-  if (!vsmp::hip_ok(hipSetDevice(dev), "hipSetDevice")) return nullptr;
+  vsmp::DeviceScope scope(dev);
+  if (!scope.ok()) return nullptr;
   vsmp_ctx* c = new vsmp_ctx();
   c->device = dev;
   c->mode = vsmp::env_mode();
@@ -731,7 +736,7 @@ vsmp_ctx* vsmp_ctx_new(int device) {
 
 void vsmp_ctx_free(vsmp_ctx* c) {
   if (!c) return;
-  (void)hipSetDevice(c->device);
+  vsmp::DeviceScope scope(c->device);
   (void)hipDeviceSynchronize();
   void* bufs[] = {c->x_flag, c->x_u,    c->x_buf,    c->s_cand, c->s_cnt,   c->s_npen,   c->s_max,
                   c->s_min,  c->s_bits, c->g_slot,   c->g_tick, c->g_npen,  c->h_probe,  c->h_full,
@@ -752,7 +757,8 @@ int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long 
                     unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
                     void* stream) {
   vsmp::clear_error();
-  if (ctx && !vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(ctx ? ctx->device : -1);
+  if (!scope.ok()) return -1;
   return vsmp::pick_batch(ctx, logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
                           out, dbg, static_cast<hipStream_t>(stream));
 }
@@ -769,7 +775,8 @@ int vsmp_pick_batch_noalloc(const float* logits, int B, int V, long long ld, con
 int vsmp_head_logits(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head, long long ldw, int B, int V,
                      int D, float* logits, long long ldl, void* stream) {
   vsmp::clear_error();
-  if (ctx && !vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(ctx ? ctx->device : -1);
+  if (!scope.ok()) return -1;
   return vsmp::head_logits(ctx, hidden, ldh, head, ldw, B, V, D, logits, ldl, static_cast<hipStream_t>(stream));
 }
 
@@ -778,7 +785,8 @@ int vsmp_head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void*
                    const double* u, unsigned long long* rng_state, unsigned long long counter, int* out, float* logits,
                    long long ldl, const vsmp_debug* dbg, void* stream) {
   vsmp::clear_error();
-  if (ctx && !vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(ctx ? ctx->device : -1);
+  if (!scope.ok()) return -1;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int rc = vsmp::head_pick(ctx, hidden, ldh, head, ldw, B, V, D, params, params_per_row, hist, hist_off, u_mode, u,
                                  rng_state, counter, out, logits, ldl, dbg, st);
@@ -793,7 +801,8 @@ int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params*
   if (!ctx || !logits || !params || !out_id) return vsmp::set_error("vsmp: null argument");
   if (n <= 0) return vsmp::set_error("vsmp: pick needs at least one logit");
   if (H < 0 || (H > 0 && !hist)) return vsmp::set_error("vsmp: bad history");
-  if (!hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(ctx->device);
+  if (!scope.ok()) return -1;
   const long long ld = (n + 3) & ~3;
   // the mapped area: [row | history | offsets | draw] then [id | diagnostics], 16-byte aligned.
   // Measured against staging it in device memory (one copy up, one back): 51 against 64 us per
@@ -851,7 +860,8 @@ int vsmp_read_probe(vsmp_ctx* ctx, const void* p, long long bytes, void* stream)
   if (!ctx || !p) return vsmp::set_error("vsmp: null argument");
   if (bytes <= 0 || bytes % 16 != 0 || reinterpret_cast<uintptr_t>(p) % 16 != 0)
     return vsmp::set_error("vsmp: read probe needs a positive multiple of 16 bytes at a 16-byte aligned address");
-  if (!vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(ctx->device);
+  if (!scope.ok()) return -1;
   if (!vsmp::grow(ctx->s_cnt, ctx->n_cnt, 8, false, "read probe sink", ctx->done_ev)) return -1;
   hipStream_t st = static_cast<hipStream_t>(stream);  // NULL: the default stream, as for vsmp_pick_batch
   vsmp::launch_read_probe(p, bytes / 16, reinterpret_cast<unsigned*>(ctx->s_cnt), 16 * ctx->cus, st);
@@ -864,7 +874,8 @@ int vsmp_exp_probe(vsmp_ctx* ctx, const double* x, double* y, long long n, void*
   if (!ctx || (n > 0 && (!x || !y))) return vsmp::set_error("vsmp: null argument");
   if (n < 0) return vsmp::set_error("vsmp: exp probe needs n >= 0");
   if (n == 0) return 0;
-  if (!vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(ctx->device);
+  if (!scope.ok()) return -1;
   vsmp::launch_exp_probe(x, y, n, static_cast<hipStream_t>(stream));
   return vsmp::hip_ok(hipGetLastError(), "exp-probe launch") ? 0 : -1;
 }
@@ -875,7 +886,8 @@ int vsmp_numer_probe(vsmp_ctx* ctx, const float* d, double* y, long long n, floa
   if (!ctx || (n > 0 && (!d || !y))) return vsmp::set_error("vsmp: null argument");
   if (n < 0 || !(temp > 0.0f) || !(qs >= 0.0f)) return vsmp::set_error("vsmp: numer probe needs n >= 0, temp > 0, qs >= 0");
   if (n == 0) return 0;
-  if (!vsmp::hip_ok(hipSetDevice(ctx->device), "hipSetDevice")) return -1;
+  vsmp::DeviceScope scope(ctx->device);
+  if (!scope.ok()) return -1;
   vsmp::launch_numer_probe(d, y, n, temp, qs, fixed_point != 0, static_cast<hipStream_t>(stream));
   return vsmp::hip_ok(hipGetLastError(), "numer-probe launch") ? 0 : -1;
 }

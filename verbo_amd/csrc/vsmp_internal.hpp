@@ -12,6 +12,35 @@ namespace vsmp {
 // false, with the calling thread's error set to "vsmp: <what>: <HIP message>", unless e is success.
 bool hip_ok(hipError_t e, const char* what);
 
+// The device a context was created on.
+int ctx_device(const vsmp_ctx* c);
+
+// An entry point's device: makes `dev` the calling thread's current HIP device for the scope, and
+// gives the caller's current device back on leaving it, so that a call leaves the thread's device
+// as it found it. ok() is false (error set) when the device could not be made current.
+class DeviceScope {
+ public:
+  explicit DeviceScope(int dev) : dev_(dev) {
+    if (dev < 0) {  // no device named (a null handle, which the entry point then rejects)
+      ok_ = true;
+      return;
+    }
+    if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+    ok_ = prev_ == dev || hip_ok(hipSetDevice(dev), "hipSetDevice");
+  }
+  ~DeviceScope() {
+    if (prev_ >= 0 && prev_ != dev_) (void)hipSetDevice(prev_);
+  }
+  DeviceScope(const DeviceScope&) = delete;
+  DeviceScope& operator=(const DeviceScope&) = delete;
+  bool ok() const { return ok_; }
+
+ private:
+  int dev_;
+  int prev_ = -1;
+  bool ok_ = false;
+};
+
 // One batched pick: the work of vsmp_pick_batch. hist_len (device-resident decode loops): row r's
 // history is hist[hist_off[r], hist_off[r] + hist_len[r]) instead of ending at hist_off[r + 1], so
 // that each row may own a region larger than its history. Returns 0 or -1 (error set).
