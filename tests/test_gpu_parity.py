@@ -374,6 +374,34 @@ def test_general_path_top_p_ties_sorted(ctx, mode):
         assert (run.info["flags"] & V.FLAG_SEQ_CUTS).any()
 
 
+@pytest.mark.parametrize("Vv", [777, 5003, 151936])
+def test_general_path_flat_rows(ctx, mode, Vv):
+    """Flat general rows (every value the same, as in padding rows), which the main pass takes
+    without its histogram atomics: top-k off and 1000, top-p off, .9 and .37, min-p off, .05 and
+    1e-30, values 0, -2.5 and 7. Half the rows carry a penalised history. The penalty leaves a row
+    of zeros flat, and turns a row of -2.5 into one of two values, which takes the pass; penalised
+    rows of 7 are zeros instead, since the penalty would take them off 7. Every comparison of the
+    parity bar against the oracle."""
+    rng = np.random.default_rng(63)
+    combos = [(0, 0.9, 0.0), (0, 1.0, 0.05), (1000, 0.9, 0.0), (1000, 0.37, 1e-30), (0, 0.37, 0.05), (1000, 1.0, 0.0)]
+    B = 2 * len(combos) * 3
+    lg = np.zeros((B, Vv), np.float32)
+    rows = []
+    for i, (tk, tp, mp) in enumerate(combos):
+        for j, val in enumerate((0.0, -2.5, 7.0)):
+            for pen in (False, True):
+                r = len(rows)
+                lg[r] = val if not (pen and val > 0) else 0.0  # a penalised positive row would not stay flat
+                rows.append(dict(temp=0.8, top_k=tk, top_p=tp, min_p=mp, repeat=1.3 if pen else 1.0, repeat_last=0,
+                                 seed=int(rng.integers(1, 1 << 62))))
+    p = V.params_array(rows)
+    h, off = csr([list(rng.integers(0, Vv, 40)) if r % 2 else [] for r in range(B)])
+    log("flat general rows", mode, Vv, B)
+    run = Run(ctx, lg, p, h, off, cand_cap=64)
+    run.report()
+    assert (run.info["keep"] == run.o_info["keep"]).all() and (run.ids == run.o_ids).all()
+
+
 def test_general_path_exp_accuracy(ctx):
     """The general path's fp64 exp (a 64-entry table method) against exp in long double: within
     1.01 ulp over [-745, 0] (the reference's libm exp is within one ulp too), exactly 1 at 0 and 0
