@@ -1540,15 +1540,41 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared<NT>& sh,
     }
     __syncthreads();
     const uint32_t klo = comp_key(clo), khi = comp_key(chi);
-    gen_pass<NT>(g.R, [&](int e, float v) {
+    // bucket of an element, or -1 when it is not in the range
+    auto bucket = [&](int e, float v) -> int {
       const uint32_t kv = ord_key(v);
-      if (kv < klo || kv > khi || !pred_v(v)) return;
+      if (kv < klo || kv > khi || !pred_v(v)) return -1;
       const uint64_t ck = comp(kv, static_cast<uint32_t>(e));
-      if (ck < clo || ck > chi || !pred_c(ck)) return;
-      const int d = static_cast<int>((ck - clo) >> shift);
-      atomicAdd(&sh.rcnt[d], 1u);
-      if (MASS) atomicAdd(&sh.rmass[d], numer_g(g, v));
-    });
+      if (ck < clo || ck > chi || !pred_c(ck)) return -1;
+      return static_cast<int>((ck - clo) >> shift);
+    };
+    // Four neighbours in one bucket (as in a row of equal values, whose buckets are ranges of
+    // indices) add with one atomic pair rather than four on one address.
+    gen_pass_groups<NT, 1>(
+        g.R,
+        [&](int e, float v) {
+          const int d = bucket(e, v);
+          if (d < 0) return;
+          atomicAdd(&sh.rcnt[d], 1u);
+          if (MASS) atomicAdd(&sh.rmass[d], numer_g(g, v));
+        },
+        [&](int e, const float (&x)[4]) {
+          int d[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) d[c] = bucket(e + c, x[c]);
+          if (d[0] >= 0 && d[0] == d[1] && d[0] == d[2] && d[0] == d[3]) {
+            atomicAdd(&sh.rcnt[d[0]], 4u);
+            if (MASS)
+              atomicAdd(&sh.rmass[d[0]], ((numer_g(g, x[0]) + numer_g(g, x[1])) + numer_g(g, x[2])) + numer_g(g, x[3]));
+            return;
+          }
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            if (d[c] < 0) continue;
+            atomicAdd(&sh.rcnt[d[c]], 1u);
+            if (MASS) atomicAdd(&sh.rmass[d[c]], numer_g(g, x[c]));
+          }
+        });
     __syncthreads();
     // scan buckets from the top (largest composites first): position p <-> bucket kRefBuckets-1-p,
     // RP consecutive positions per thread
@@ -1856,7 +1882,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   // every element in bucket 0 with the numerator exp(0) = 1 (fixed point 2^40, numer_fix): its
   // histogram, min-p count and prefix are known without the pass, whose atomics would all meet on
   // one address (256 x 151,936 zeros, top-p .9: 1,063 to 809 us per call, against 115 us for rows
-  // of normal values; the selects after it still refine that one bucket over the row's indices).
+  // of normal values; the selects after it refine that one bucket over the row's indices).
   // With a top-k cut the kept elements are the first k by index (equal values rank by index).
   const bool flat = comp_key(mxc) == static_cast<uint32_t>(mnk) && isfinite(g.mx);
   // one instance per combination without a top-k restriction (the common case: no per-element
