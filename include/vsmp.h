@@ -124,8 +124,11 @@ VSMP_API void vsmp_ctx_free(vsmp_ctx* ctx);
  *   u_mode/u/rng_state/counter: see vsmp_u_mode (unused pointers may be NULL).
  *   out: device int[B] picked ids.
  *   dbg: optional diagnostic outputs (HOST pointer to a vsmp_debug, or NULL).
- * Calls that share a context must be issued from one host thread; calls on different streams
- * with one context must not overlap. Returns 0, or -1 (bad arguments, HIP error). */
+ * Calls that share a context must be issued from one host thread. A call on another stream than
+ * the context's previous call must be ordered after that call (the new stream waits for an event
+ * recorded after it, or the host synchronised): a call that needs more scratch than any before it
+ * waits for its own stream only, then replaces buffers the earlier calls used. `stream` must belong
+ * to the context's device. Returns 0, or -1 (bad arguments, HIP error). */
 VSMP_API int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
                              const vsmp_params* params, int params_per_row, const int* hist,
                              const int* hist_off, int u_mode, const double* u,
@@ -140,7 +143,9 @@ VSMP_API int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, l
  * and sort slot) is one static device array of 4,218,880 bytes per GPU, held until the process
  * ends and shared by every call on that GPU: calls that overlap on one GPU (on different streams,
  * or from different threads) race and must not be issued. Per-row parameter batches run their
- * general rows after the row kernel on `stream` (no second stream). Returns 0 or -1. */
+ * general rows after the row kernel on `stream` (no second stream). The call runs on the stream's
+ * device (the null stream: the calling thread's current device), with that device's copy of the
+ * array. Returns 0 or -1. */
 VSMP_API int vsmp_pick_batch_noalloc(const float* logits, int B, int V, long long ld,
                                      const vsmp_params* params, int params_per_row, const int* hist,
                                      const int* hist_off, int u_mode, const double* u,
@@ -237,7 +242,9 @@ typedef struct vsmp_dsampler vsmp_dsampler;
 /* Sampler::Sampler(Sampling), src/sampler.cpp:24. NULL on error. */
 VSMP_API vsmp_dsampler* vsmp_dsampler_new(int device, const vsmp_params* cfg);
 VSMP_API void vsmp_dsampler_free(vsmp_dsampler* s);
-/* Sampler::reset, src/sampler.cpp:26-31 (reseeds; clears the history). Returns 0 or -1. */
+/* Sampler::reset, src/sampler.cpp:26-31 (reseeds; clears the history). Waits for the device first,
+ * so that picks and accepts still queued on any stream finish before the state is replaced.
+ * Returns 0 or -1. */
 VSMP_API int vsmp_dsampler_reset(vsmp_dsampler* s);
 /* Sampler::accept for ids[0..n) in order (host array, e.g. a prompt), stream-ordered on
  * `stream`. Returns 0 or -1. */

@@ -429,7 +429,8 @@ class Sampler:
 
     def pick(self, logits):
         lg = np.ascontiguousarray(logits, dtype=np.float32)
-        r = _lib.vsmp_sampler_pick(self._h, lg.ctypes.data_as(_P), lg.size)
+        # the address as a plain int: ndarray.ctypes.data_as builds several objects per call
+        r = _lib.vsmp_sampler_pick(self._h, lg.ctypes.data, lg.size)
         if r < 0:
             raise _err()
         return r

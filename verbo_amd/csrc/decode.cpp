@@ -147,6 +147,9 @@ int vsmp_dsampler_reset(vsmp_dsampler* s) {
   if (!s) return vsmp::set_error("vsmp: null sampler");
   vsmp::DeviceScope scope(s->device);
   if (!scope.ok()) return -1;
+  // Picks and accepts still queued on the caller's streams advance the draw stream and the window in
+  // place; the reset must land after them, and it has no stream of its own: wait for the device.
+  if (!hip_ok(hipDeviceSynchronize(), "synchronise")) return -1;
   std::uint64_t st[2];
   vsmp::seed_stream(s->cfg.seed, st);
   if (!hip_ok(hipMemcpy(s->rng, st, sizeof st, hipMemcpyHostToDevice), "copy draw stream")) return -1;

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
+#include <climits>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -35,14 +37,17 @@ bool hip_ok(hipError_t e, const char* what) {
 
 namespace {
 
-// Grows a context buffer to `need` elements. The old buffer is freed once the device has finished
-// every call that may still use it: growing waits for the device (calls on any stream), which
-// happens only when a call needs more scratch than any call before it on the context. (An event
-// recorded after every call, waited for here instead, cost each call issued one by one about 3 us
-// of GPU time: 34.1 against 31.2 us at 256 x 151,936, 14.9 against 12.0 at 1 x 1024.)
-// A buffer that must start at zero is cleared on `zst`, the stream of the call that will use it.
+// Grows a context buffer to `need` elements. The old buffer is freed once every call that may still
+// use it has finished: growing waits for `st`, the stream of the call that will use the new buffer.
+// That covers every earlier call of the context: those issued on `st` (their side-stream work is
+// joined back into it), and those on other streams, which vsmp_pick_batch requires the caller to
+// order before this call (so `st` completes after them). Growth happens only when a call needs more
+// scratch than any call before it on the context. No device-wide wait: it would also wait for other
+// threads' streams and break a global-mode graph capture running elsewhere. (An event recorded after
+// every call, waited for here instead, cost each call issued one by one about 3 us of GPU time: 34.1
+// against 31.2 us at 256 x 151,936.) A buffer that must start at zero is cleared on `st`.
 template <class T>
-bool grow(T*& p, size_t& cap, size_t need, bool zero, const char* what, hipStream_t zst = nullptr) {
+bool grow(T*& p, size_t& cap, size_t need, bool zero, const char* what, hipStream_t st) {
   if (need <= cap && p) return true;
   // doubling spares small buffers repeated growth as a batch widens; a large one is sized to the
   // request, so that what a call asks for bounds what the context holds
@@ -50,14 +55,14 @@ bool grow(T*& p, size_t& cap, size_t need, bool zero, const char* what, hipStrea
   size_t n = need;
   if (need < small) n = std::min(std::max(need, cap * 2), small);
   if (p) {
-    if (!hip_ok(hipDeviceSynchronize(), "wait for the device before growing scratch")) return false;
+    if (!hip_ok(hipStreamSynchronize(st), "wait for the stream before growing scratch")) return false;
     (void)hipFree(p);
     p = nullptr;
     cap = 0;
   }
   void* q = nullptr;
   if (!hip_ok(hipMalloc(&q, n * sizeof(T)), what)) return false;
-  if (zero && !hip_ok(hipMemsetAsync(q, 0, n * sizeof(T), zst), what)) {
+  if (zero && !hip_ok(hipMemsetAsync(q, 0, n * sizeof(T), st), what)) {
     (void)hipFree(q);
     return false;
   }
@@ -135,9 +140,16 @@ struct vsmp_ctx {
   // space (hs_dev), holding the row, the history, its offsets and the draw, then the id and the row
   // diagnostics: the kernels read their inputs from it and write their results into it, with no
   // copy either way
-  unsigned char* hs_host = nullptr;
-  unsigned char* hs_dev = nullptr;
+  // Two such areas, used in turn: a greedy or small-k pick returns as soon as its id is in host
+  // memory, before its stream has finished (host_ev, recorded after its kernels, then marks that
+  // point, and the next batched call on the context waits for it on the GPU). The area a pick fills
+  // was last used two picks before, whose kernels ended before the previous pick's started.
+  unsigned char* hs_host[2] = {nullptr, nullptr};
+  unsigned char* hs_dev[2] = {nullptr, nullptr};
   size_t n_hs = 0;
+  int hs_next = 0;
+  hipEvent_t host_ev = nullptr;
+  bool host_pending = false;  // a host pick returned before its stream finished
 };
 
 namespace vsmp {
@@ -361,23 +373,23 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
   const size_t slots = static_cast<size_t>(B) * static_cast<size_t>(pl.S);
   if (slots > static_cast<size_t>(INT32_MAX) / kKmax) return set_error("vsmp: batch too large");
   const int words = a.words;
-  if (!grow(ctx->s_cnt, ctx->n_cnt, slots, false, "scratch") ||
-      !grow(ctx->s_npen, ctx->n_npen, slots, false, "scratch") ||
-      !grow(ctx->s_max, ctx->n_max, slots, false, "scratch") ||
-      !grow(ctx->s_min, ctx->n_min, slots, false, "scratch"))
+  if (!grow(ctx->s_cnt, ctx->n_cnt, slots, false, "scratch", st) ||
+      !grow(ctx->s_npen, ctx->n_npen, slots, false, "scratch", st) ||
+      !grow(ctx->s_max, ctx->n_max, slots, false, "scratch", st) ||
+      !grow(ctx->s_min, ctx->n_min, slots, false, "scratch", st))
     return -1;
-  if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch")) return -1;
+  if (pl.any_smallk && !grow(ctx->s_cand, ctx->n_cand, slots * kKmax, false, "scratch", st)) return -1;
   // General rows marked near a top-p tie are redone exactly (rows up to kExactMaxVocab). The scratch
   // is sized whenever a batch may hold general rows, whatever its parameters, so that one call at a
   // shape sizes it for every later call at that shape (graph capture); the launch is skipped for
   // shared parameters without a top-p cut, which mark no row.
   const bool exact_scratch = pl.any_general && V <= kExactMaxVocab;
   const bool exact = exact_scratch && (params_per_row || (params->top_p > 0.0f && params->top_p < 1.0f));
-  if (exact_scratch && (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch") ||
-                        !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch") ||
-                        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(exact_slots(a.x_n, B)) * 2 * a.x_n, false, "scratch")))
+  if (exact_scratch && (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch", st) ||
+                        !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch", st) ||
+                        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(exact_slots(a.x_n, B)) * 2 * a.x_n, false, "scratch", st)))
     return -1;
-  if (pl.any_general && !pl.rows && !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch"))
+  if (pl.any_general && !pl.rows && !grow(ctx->s_bits, ctx->n_bits, static_cast<size_t>(B) * words, false, "scratch", st))
     return -1;
   if (a.pen_bits) {  // diagnostics: the kernels store or OR each row's penalised ids into zeroed bitmaps
     launch_zero_u32(a.pen_bits, static_cast<long long>(B) * words, st);
@@ -457,11 +469,21 @@ int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld,
 
 }  // namespace
 
+// A host pick that returned before its stream finished is ordered before the context's next work on
+// another stream (its kernels may still be completing, and that work may reuse their scratch).
+bool after_host_pick(vsmp_ctx* ctx, hipStream_t st) {
+  if (!ctx->host_pending || st == ctx->stream) return true;
+  if (!hip_ok(hipStreamWaitEvent(st, ctx->host_ev, 0), "hipStreamWaitEvent")) return false;
+  ctx->host_pending = false;
+  return true;
+}
+
 int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
                int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
                unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
                hipStream_t st, const int* hist_len) {
   if (!ctx) return set_error("vsmp: null context");
+  if (!after_host_pick(ctx, st)) return -1;
   return launch_batch(ctx, logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter, out,
                       dbg, st, hist_len);
 }
@@ -503,6 +525,7 @@ HeadArgs head_args(const void* hidden, long long ldh, const void* head, long lon
 
 int head_logits(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head, long long ldw, int B, int V, int D,
                 float* logits, long long ldl, hipStream_t st) {
+  if (ctx && !after_host_pick(ctx, st)) return -1;
   if (!ctx) return set_error("vsmp: null context");
   if (!logits) return set_error("vsmp: logits is required");
   if (check_head(hidden, ldh, head, ldw, B, V, D, logits, ldl, false) != 0) return -1;
@@ -519,6 +542,7 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
               const vsmp_params* params, int params_per_row, const int* hist, const int* hist_off, int u_mode,
               const double* u, unsigned long long* rng_state, unsigned long long counter, int* out, float* logits,
               long long ldl, const vsmp_debug* dbg, hipStream_t st) {
+  if (ctx && !after_host_pick(ctx, st)) return -1;
   if (!ctx) return set_error("vsmp: null context");
   if (check_head(hidden, ldh, head, ldw, B, V, D, logits, ldl, true) != 0) return -1;
   if (!out || !params) return set_error("vsmp: params and out are required");
@@ -546,7 +570,7 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
   long long fld = ldl;
   if (!full && (whole || params_per_row)) {
     fld = (static_cast<long long>(V) + 3) & ~3LL;
-    if (!grow(ctx->h_full, ctx->n_full, static_cast<size_t>(B) * static_cast<size_t>(fld), false, "head scratch"))
+    if (!grow(ctx->h_full, ctx->n_full, static_cast<size_t>(B) * static_cast<size_t>(fld), false, "head scratch", st))
       return -1;
     full = ctx->h_full;
   }
@@ -563,11 +587,11 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
   }
   const int n0 = std::min(kHeadProbe, V);
   const int tile = head_tile(B, false);
-  if (!grow(ctx->h_tk, ctx->n_tk, static_cast<size_t>(B), false, "head scratch") ||
-      !grow(ctx->h_rmode, ctx->n_rmode, static_cast<size_t>(B), false, "head scratch") ||
-      !grow(ctx->h_rcand, ctx->n_rcand, static_cast<size_t>(B) * static_cast<size_t>(V), false, "head scratch") ||
-      !grow(ctx->h_rcnt, ctx->n_rcnt, static_cast<size_t>(B), false, "head scratch") ||
-      (!full && !grow(ctx->h_probe, ctx->n_probe, static_cast<size_t>(B) * static_cast<size_t>(n0), false, "head scratch")))
+  if (!grow(ctx->h_tk, ctx->n_tk, static_cast<size_t>(B), false, "head scratch", st) ||
+      !grow(ctx->h_rmode, ctx->n_rmode, static_cast<size_t>(B), false, "head scratch", st) ||
+      !grow(ctx->h_rcand, ctx->n_rcand, static_cast<size_t>(B) * static_cast<size_t>(V), false, "head scratch", st) ||
+      !grow(ctx->h_rcnt, ctx->n_rcnt, static_cast<size_t>(B), false, "head scratch", st) ||
+      (!full && !grow(ctx->h_probe, ctx->n_probe, static_cast<size_t>(B) * static_cast<size_t>(n0), false, "head scratch", st)))
     return -1;
   float* probe = full ? full : ctx->h_probe;
   const long long pld = full ? fld : n0;
@@ -613,9 +637,9 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
   if (!hip_ok(hipGetLastError(), "finish launch")) return -1;
   // 5. general rows (per-row parameters): the general path over their written logits
   if (params_per_row) {
-    if (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch") ||
-        !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch") ||
-        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(exact_slots(a.x_n, B)) * 2 * a.x_n, false, "scratch"))
+    if (!grow(ctx->x_flag, ctx->n_xflag, static_cast<size_t>(B), false, "scratch", st) ||
+        !grow(ctx->x_u, ctx->n_xu, static_cast<size_t>(B), false, "scratch", st) ||
+        !grow(ctx->x_buf, ctx->n_xbuf, static_cast<size_t>(exact_slots(a.x_n, B)) * 2 * a.x_n, false, "scratch", st))
       return -1;
     a.x_flag = ctx->x_flag;
     a.x_u = ctx->x_u;
@@ -682,6 +706,19 @@ int pick_batch_noalloc(const float* logits, int B, int V, long long ld, const vs
 
 namespace vsmp {
 int ctx_device(const vsmp_ctx* c) { return c->device; }
+
+// A stream passed with a context must belong to the context's device (its scratch lives there).
+bool stream_on_device(const vsmp_ctx* c, hipStream_t st) {
+  if (!c || !st) return true;  // a null context is rejected by the call; the null stream is the device's own
+  hipDevice_t d = 0;
+  if (!hip_ok(hipStreamGetDevice(st, &d), "device of the stream")) return false;
+  if (static_cast<int>(d) != c->device) {
+    set_error("vsmp: the stream belongs to device " + std::to_string(d) + ", the context to device " +
+              std::to_string(c->device));
+    return false;
+  }
+  return true;
+}
 }  // namespace vsmp
 
 extern "C" {
@@ -713,7 +750,8 @@ vsmp_ctx* vsmp_ctx_new(int device) {
   if (!vsmp::hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate") ||
       !vsmp::hip_ok(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking), "hipStreamCreate") ||
       !vsmp::hip_ok(hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming), "hipEventCreate") ||
-      !vsmp::hip_ok(hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming), "hipEventCreate")) {
+      !vsmp::hip_ok(hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming), "hipEventCreate") ||
+      !vsmp::hip_ok(hipEventCreateWithFlags(&c->host_ev, hipEventDisableTiming), "hipEventCreate")) {
     vsmp_ctx_free(c);
     return nullptr;
   }
@@ -729,7 +767,9 @@ void vsmp_ctx_free(vsmp_ctx* c) {
                   c->h_tk,   c->h_rmode, c->h_rcand, c->h_rcnt};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
-  if (c->hs_host) (void)hipHostFree(c->hs_host);
+  for (unsigned char* h : c->hs_host)
+    if (h) (void)hipHostFree(h);
+  if (c->host_ev) (void)hipEventDestroy(c->host_ev);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   if (c->side) (void)hipStreamDestroy(c->side);
   if (c->fork_ev) (void)hipEventDestroy(c->fork_ev);
@@ -743,7 +783,7 @@ int vsmp_pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long 
                     void* stream) {
   vsmp::clear_error();
   vsmp::DeviceScope scope(ctx ? ctx->device : -1);
-  if (!scope.ok()) return -1;
+  if (!scope.ok() || !vsmp::stream_on_device(ctx, static_cast<hipStream_t>(stream))) return -1;
   return vsmp::pick_batch(ctx, logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
                           out, dbg, static_cast<hipStream_t>(stream));
 }
@@ -753,6 +793,16 @@ int vsmp_pick_batch_noalloc(const float* logits, int B, int V, long long ld, con
                             unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
                             void* stream) {
   vsmp::clear_error();
+  // The call runs on the stream's device, whose copy of the static scratch it must take: that
+  // device is made current for the call (the null stream: the calling thread's current device).
+  int dev = -1;
+  if (stream) {
+    hipDevice_t d = 0;
+    if (!vsmp::hip_ok(hipStreamGetDevice(static_cast<hipStream_t>(stream), &d), "device of the stream")) return -1;
+    dev = static_cast<int>(d);
+  }
+  vsmp::DeviceScope scope(dev);
+  if (!scope.ok()) return -1;
   return vsmp::pick_batch_noalloc(logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
                                   out, dbg, static_cast<hipStream_t>(stream));
 }
@@ -761,7 +811,7 @@ int vsmp_head_logits(vsmp_ctx* ctx, const void* hidden, long long ldh, const voi
                      int D, float* logits, long long ldl, void* stream) {
   vsmp::clear_error();
   vsmp::DeviceScope scope(ctx ? ctx->device : -1);
-  if (!scope.ok()) return -1;
+  if (!scope.ok() || !vsmp::stream_on_device(ctx, static_cast<hipStream_t>(stream))) return -1;
   return vsmp::head_logits(ctx, hidden, ldh, head, ldw, B, V, D, logits, ldl, static_cast<hipStream_t>(stream));
 }
 
@@ -771,7 +821,7 @@ int vsmp_head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void*
                    long long ldl, const vsmp_debug* dbg, void* stream) {
   vsmp::clear_error();
   vsmp::DeviceScope scope(ctx ? ctx->device : -1);
-  if (!scope.ok()) return -1;
+  if (!scope.ok() || !vsmp::stream_on_device(ctx, static_cast<hipStream_t>(stream))) return -1;
   return vsmp::head_pick(ctx, hidden, ldh, head, ldw, B, V, D, params, params_per_row, hist, hist_off, u_mode, u,
                          rng_state, counter, out, logits, ldl, dbg, static_cast<hipStream_t>(stream));
 }
@@ -785,6 +835,7 @@ int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params*
   if (H < 0 || (H > 0 && !hist)) return vsmp::set_error("vsmp: bad history");
   vsmp::DeviceScope scope(ctx->device);
   if (!scope.ok()) return -1;
+  hipStream_t st = ctx->stream;
   const long long ld = (n + 3) & ~3;
   // the mapped area: [row | history | offsets | draw] then [id | diagnostics], 16-byte aligned.
   // Measured against staging it in device memory (one copy up, one back): 51 against 64 us per
@@ -797,30 +848,35 @@ int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params*
   const size_t o_info = o_out + 16;
   const size_t total = o_info + up16(sizeof(vsmp_row_info));
   if (total > ctx->n_hs) {
-    // every call ends synchronised, so the old area is idle here
-    if (ctx->hs_host) (void)hipHostFree(ctx->hs_host);
-    ctx->hs_host = nullptr;
-    ctx->hs_dev = nullptr;
-    ctx->n_hs = 0;
-    void* h = nullptr;
-    void* d = nullptr;
-    if (!hip_ok(hipHostMalloc(&h, total, hipHostMallocMapped), "host-path staging")) return -1;
-    if (!hip_ok(hipHostGetDevicePointer(&d, h, 0), "host-path device address")) {
-      (void)hipHostFree(h);
-      return -1;
+    // a pick that returned early may still be finishing on the stream
+    if (!hip_ok(hipStreamSynchronize(st), "synchronise")) return -1;
+    for (int i = 0; i < 2; ++i) {
+      if (ctx->hs_host[i]) (void)hipHostFree(ctx->hs_host[i]);
+      ctx->hs_host[i] = nullptr;
+      ctx->hs_dev[i] = nullptr;
     }
-    ctx->hs_host = static_cast<unsigned char*>(h);
-    ctx->hs_dev = static_cast<unsigned char*>(d);
+    ctx->n_hs = 0;
+    for (int i = 0; i < 2; ++i) {
+      void* h = nullptr;
+      void* d = nullptr;
+      if (!hip_ok(hipHostMalloc(&h, total, hipHostMallocMapped), "host-path staging")) return -1;
+      ctx->hs_host[i] = static_cast<unsigned char*>(h);
+      if (!hip_ok(hipHostGetDevicePointer(&d, h, 0), "host-path device address")) return -1;
+      ctx->hs_dev[i] = static_cast<unsigned char*>(d);
+    }
     ctx->n_hs = total;
   }
-  unsigned char* hs = ctx->hs_host;
-  unsigned char* ds = ctx->hs_dev;
+  const int area = ctx->hs_next;
+  ctx->hs_next ^= 1;
+  unsigned char* hs = ctx->hs_host[area];
+  unsigned char* ds = ctx->hs_dev[area];
   std::memcpy(hs, logits, sizeof(float) * static_cast<size_t>(n));
   if (H > 0) std::memcpy(hs + o_hist, hist, sizeof(int) * static_cast<size_t>(H));
   const int hoff[2] = {0, H};
   std::memcpy(hs + o_hoff, hoff, sizeof hoff);
   std::memcpy(hs + o_u, &u, sizeof u);
-  hipStream_t st = ctx->stream;
+  volatile int* id_slot = reinterpret_cast<volatile int*>(hs + o_out);  // the kernels write an id >= 0
+  *id_slot = INT_MIN;
   vsmp_debug dbg{};
   dbg.info = reinterpret_cast<vsmp_row_info*>(ds + o_info);
   if (vsmp::pick_batch(ctx, reinterpret_cast<const float*>(ds), 1, n, ld, params, 0,
@@ -831,7 +887,30 @@ int vsmp_pick_host(vsmp_ctx* ctx, const float* logits, int n, const vsmp_params*
     (void)hipStreamSynchronize(st);  // what was queued still reads the area the next call refills
     return -1;
   }
-  if (!hip_ok(hipStreamSynchronize(st), "synchronise")) return -1;
+  // A greedy or small-k row without diagnostics has its id written once, by the last kernel of the
+  // pick, after every read of the area: the call returns as soon as the id is in host memory. The
+  // stream's completion reaches the host about 5 us after that (a pick on a 49,152-logit row: 25.0
+  // us to the id, 30.5 us to the completion, whichever way it is waited for). Other picks (the
+  // general path may redo the row in a second kernel; diagnostics follow the id) wait for the stream.
+  // A pick whose id is not there within 2 ms leaves the rest of the wait to the stream too.
+  const int path = vsmp::path_host(*params, n, true);
+  const bool one_writer =
+      !info && (path == vsmp::kPathGreedy || (path == vsmp::kPathSmallK && n <= vsmp::kRowMaxVocab && ctx->mode != 0));
+  bool done = false;
+  if (one_writer) {
+    if (!hip_ok(hipEventRecord(ctx->host_ev, st), "hipEventRecord")) {
+      (void)hipStreamSynchronize(st);
+      return -1;
+    }
+    ctx->host_pending = true;
+    const auto t0 = std::chrono::steady_clock::now();
+    while (!(done = *id_slot != INT_MIN) && std::chrono::steady_clock::now() - t0 < std::chrono::milliseconds(2)) {
+    }
+  }
+  if (!done) {
+    if (!hip_ok(hipStreamSynchronize(st), "synchronise")) return -1;
+    ctx->host_pending = false;
+  }
   std::memcpy(out_id, hs + o_out, sizeof(int));
   if (info) std::memcpy(info, hs + o_info, sizeof(vsmp_row_info));
   return 0;
@@ -844,8 +923,8 @@ int vsmp_read_probe(vsmp_ctx* ctx, const void* p, long long bytes, void* stream)
     return vsmp::set_error("vsmp: read probe needs a positive multiple of 16 bytes at a 16-byte aligned address");
   vsmp::DeviceScope scope(ctx->device);
   if (!scope.ok()) return -1;
-  if (!vsmp::grow(ctx->s_cnt, ctx->n_cnt, 8, false, "read probe sink")) return -1;
   hipStream_t st = static_cast<hipStream_t>(stream);  // NULL: the default stream, as for vsmp_pick_batch
+  if (!vsmp::after_host_pick(ctx, st) || !vsmp::grow(ctx->s_cnt, ctx->n_cnt, 8, false, "read probe sink", st)) return -1;
   vsmp::launch_read_probe(p, bytes / 16, reinterpret_cast<unsigned*>(ctx->s_cnt), 16 * ctx->cus, st);
   return vsmp::hip_ok(hipGetLastError(), "read-probe launch") ? 0 : -1;
 }

@@ -84,12 +84,13 @@ void launch_general(const KArgs& a, int cus, hipStream_t st);
 void launch_general_exact(const KArgs& a, int slots, hipStream_t st);
 void launch_numer_probe(const float* d, double* y, long long n, float temp, float qs, bool fixed_point, hipStream_t st);
 // Workgroups (and scratch slots of 2 * x_n entries) of k_general_exact for a batch of B rows: one
-// per row up to 256 (one per CU, so that a batch whose rows are all marked is redone in parallel),
-// at least 8, within 1 GB of slots (256 slots of 4 MB at 151,936 logits, 64 of 16 MB at 2^20); the
-// context sizes a scratch buffer this large to the request.
+// per row up to 256, at least 8, within 256 MiB of slots (64 slots of 4 MiB at 151,936 logits, 16
+// of 16 MiB at 2^20); the context sizes a scratch buffer this large to the request. The marked rows
+// (rows whose top-p cut lay within rounding distance of top_p) are dealt to the slots in turn, so a
+// batch with more marked rows than slots redoes them in rounds.
 inline int exact_slots(int x_n, int B) {
   const long long per = 16LL * x_n;
-  const long long budget = (1LL << 30) / per;
+  const long long budget = (1LL << 28) / per;
   long long n = B < 8 ? 8 : (B > 256 ? 256 : B);
   if (n > budget) n = budget;
   return static_cast<int>(n < 1 ? 1 : n);

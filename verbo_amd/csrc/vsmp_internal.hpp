@@ -14,6 +14,9 @@ bool hip_ok(hipError_t e, const char* what);
 
 // The device a context was created on.
 int ctx_device(const vsmp_ctx* c);
+// true when `st` (null: the device's null stream) belongs to the context's device; else false, with
+// the error set.
+bool stream_on_device(const vsmp_ctx* c, hipStream_t st);
 
 // An entry point's device: makes `dev` the calling thread's current HIP device for the scope, and
 // gives the caller's current device back on leaving it, so that a call leaves the thread's device

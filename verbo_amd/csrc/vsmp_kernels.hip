@@ -2478,6 +2478,7 @@ __device__ void exact_flat_row(const KArgs& a, int row, const vsmp_params& P, in
 __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
   __shared__ int list[kGenThreads];
   __shared__ int nlist;
+  __shared__ int wmarked[kGenThreads / 64];
   __shared__ int xkeep;
   __shared__ double xd[8];
   __shared__ int xi[4];
@@ -2488,13 +2489,27 @@ __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
   const int V = a.V, n2 = a.x_n;
   uint64_t* xs = reinterpret_cast<uint64_t*>(a.x_buf) + static_cast<size_t>(blockIdx.x) * 2 * static_cast<size_t>(n2);
   double* pr = reinterpret_cast<double*>(xs + n2);
-  for (int c0 = blockIdx.x; c0 < a.B; c0 += gridDim.x * kGenThreads) {
+  // The marked rows, in row order, are dealt to the workgroups in turn (the m-th to workgroup m mod
+  // grid), so that however few slots the batch has, marked rows are spread evenly over them and no
+  // other row costs more than its flag read.
+  int seen = 0;  // marked rows before this chunk of the batch
+  for (int c0 = 0; c0 < a.B; c0 += kGenThreads) {
     if (tid == 0) nlist = 0;
-    __syncthreads();
     {
-      const int r = c0 + static_cast<int>(gridDim.x) * tid;
-      if (r < a.B && a.x_flag[r] != 0 && path_of(row_params(a, r), V, a.smallk_ok) == kPathGeneral)
-        list[atomicAdd(&nlist, 1)] = r;
+      const int r = c0 + tid;
+      const bool m = r < a.B && a.x_flag[r] != 0 && path_of(row_params(a, r), V, a.smallk_ok) == kPathGeneral;
+      const uint64_t bal = __ballot(m);
+      const int lane = tid & 63, w = tid >> 6;
+      if (lane == 0) wmarked[w] = __popcll(bal);
+      __syncthreads();
+      int before = 0, total = 0;
+      for (int i = 0; i < kGenThreads / 64; ++i) {
+        before += i < w ? wmarked[i] : 0;
+        total += wmarked[i];
+      }
+      const int idx = seen + before + __popcll(bal & ((1ull << lane) - 1ull));
+      if (m && idx % static_cast<int>(gridDim.x) == static_cast<int>(blockIdx.x)) list[atomicAdd(&nlist, 1)] = r;
+      seen += total;
     }
     __syncthreads();
     const int nmarked = nlist;
@@ -3525,16 +3540,17 @@ __global__ __launch_bounds__(kTkNT) void k_topk_split(KArgs a) {
   __syncthreads();
   if (tid == 0) {
     const unsigned t = __hip_atomic_fetch_add(&a.g_tick[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh.ints[9] = t == static_cast<unsigned>(a.P - 1);
+    const bool last = t == static_cast<unsigned>(a.P - 1);
+    // The last part: every other part's lists and counts were stored with agent-scope stores and had
+    // completed (vmcnt(0)) before that part's ticket, whose read-modify-write returned P - 1 to this
+    // part only after all of them. An agent-scope acquire here, as k_greedy_split's last part takes,
+    // drops what this CU's and this XCD's caches hold of them, so the merge below (agent-scope loads,
+    // ordered after it by the barrier) cannot be served a line read before the ticket.
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    sh.ints[9] = last;
   }
   __syncthreads();
   if (!sh.ints[9]) return;
-  // The last part: every other part's lists and counts were stored with agent-scope stores
-  // (written through to the memory side, past the XCDs' L2s) and had completed (vmcnt(0)) before
-  // that part's ticket; the ticket's read-modify-write, performed at the memory side, returned P - 1
-  // to this part only after all of them; the merge reads them with agent-scope loads, which bypass
-  // the L2 as well. An acquire fence here (buffer_inv sc1: the XCD's L2 dropped) added 1.5-3.7 us at
-  // 1-24 rows of 151,936 (the other parts' data leaving that L2) and is not taken.
   if (tid == 0) __hip_atomic_store(&a.g_tick[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   finish_smallk<kTkNT, true>(a, row, P, a.P, sh.mbuf, sh.top, sh.red64, sh.ints, sh.off);
 }
