@@ -276,6 +276,33 @@ VSMP_API int vsmp_bsampler_accept(vsmp_bsampler* s, const int* ids, const int* a
  * dropped), else 0; waits for `stream`. -1 on error. */
 VSMP_API int vsmp_bsampler_full(vsmp_bsampler* s, void* stream);
 
+/* ---- continuous batching: slots that sequences take in turn -------------------------------------
+ * The reference's server takes one request at a time (cli/serve.cpp:139-192: a request's options
+ * become GenOpts, generate runs, under one mutex, :168). Here the n rows of a vsmp_bsampler are
+ * slots: a finished sequence's slot is given to the next request, and each step samples only the
+ * live slots. A slot's sequence is a verbo::Sampler of its own throughout: its draws and picks are
+ * those the reference's Sampler gives when it decodes that request alone. */
+
+/* A new sequence takes slot `slot` (stream-ordered on `stream`, after the slot's earlier picks and
+ * accepts): verbo::Sampler(*params) (src/sampler.cpp:24-31: the draw stream seeded from
+ * params->seed, 0 standing for the clock) followed by accept() of each id of the host array
+ * prompt[0..m) (src/sampler.cpp:43-48), which is read before the call returns. params->repeat_last
+ * must fit the slots' regions (4 * repeat_last <= cap), as must the window the prompt leaves.
+ * Returns 0 or -1. */
+VSMP_API int vsmp_bsampler_admit(vsmp_bsampler* s, int slot, const vsmp_params* params, const int* prompt, int m,
+                                 void* stream);
+/* One pick for each of the n_rows live slots rows[0..n_rows) (device array of distinct slots), from
+ * device logits [n_rows][ld] (row i for slot rows[i], V logits per row), ids to device out[n_rows],
+ * on `stream`. Each pick is Sampler::pick of that slot's sequence (src/sampler.cpp:50-109) with
+ * the slot's parameters, history and draw stream; slots not listed are neither read nor advanced.
+ * n_rows = 0 does nothing. Returns 0 or -1. */
+VSMP_API int vsmp_bsampler_pick_rows(vsmp_bsampler* s, const float* logits, int V, long long ld, const int* rows,
+                                     int n_rows, int* out, void* stream);
+/* Sampler::accept of device ids[i] into slot rows[i] for every i < n_rows with active[i] != 0
+ * (device arrays; active NULL: every entry), on `stream`. Returns 0 or -1. */
+VSMP_API int vsmp_bsampler_accept_rows(vsmp_bsampler* s, const int* ids, const int* rows, const int* active,
+                                       int n_rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,7 +19,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = V.load_library()
     names = declared_symbols()
-    assert len(names) == 29, names
+    assert len(names) == 32, names
     for n in names:
         assert hasattr(lib, n), n
 

@@ -177,8 +177,8 @@ int vsmp_dsampler_accept(vsmp_dsampler* s, const int* ids, int n, void* stream) 
   // otherwise the window keeps some of its ids: append one by one on the device
   for (int i = 0; i < n; ++i) {
     if (rl <= 0 && !ds_reserve(s, s->h + 1, st)) return -1;
-    vsmp::launch_hist_accept(s->hist, s->meta, s->meta + 1, s->cap, nullptr, s->cfg, nullptr, ids[i], nullptr, 1, nullptr,
-                             st);
+    vsmp::launch_hist_accept(s->hist, s->meta, s->meta + 1, s->cap, nullptr, s->cfg, nullptr, ids[i], nullptr, nullptr, 1,
+                             nullptr, st);
     if (!hip_ok(hipGetLastError(), "accept launch")) return -1;
     s->h = accepted_length(s->h, 1, rl);
   }
@@ -336,8 +336,61 @@ int vsmp_bsampler_accept(vsmp_bsampler* s, const int* ids, const int* active, vo
   if (!s || !ids) return vsmp::set_error("vsmp: bad accept arguments");
   vsmp::DeviceScope scope(s->device);
   if (!scope.ok()) return -1;
-  vsmp::launch_hist_accept(s->hist, s->off, s->len, s->cap, s->params, vsmp_params{}, ids, 0, active, s->n, s->full,
-                           static_cast<hipStream_t>(stream));
+  vsmp::launch_hist_accept(s->hist, s->off, s->len, s->cap, s->params, vsmp_params{}, ids, 0, active, nullptr, s->n,
+                           s->full, static_cast<hipStream_t>(stream));
+  return hip_ok(hipGetLastError(), "accept launch") ? 0 : -1;
+}
+
+int vsmp_bsampler_admit(vsmp_bsampler* s, int slot, const vsmp_params* params, const int* prompt, int m, void* stream) {
+  vsmp::clear_error();
+  if (!s || !params || slot < 0 || slot >= s->n || m < 0 || (m > 0 && !prompt))
+    return vsmp::set_error("vsmp: bad admit arguments");
+  const vsmp_params p = *params;
+  if (p.repeat_last > 0 && static_cast<long long>(p.repeat_last) * 4 > s->cap)
+    return vsmp::set_error("vsmp: cap must hold 4 * repeat_last ids");
+  // Sampler(cfg) then accept() of each prompt id (src/sampler.cpp:24-48): the window the prompt
+  // leaves is its last `len` ids
+  const int len = accepted_length(0, m, p.repeat_last);
+  if (len > s->cap) return vsmp::set_error("vsmp: the prompt's history window is longer than the slot's region");
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok()) return -1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  std::uint64_t rs[2];
+  vsmp::seed_stream(p.seed, rs);
+  if (!p.seed) rs[0] += static_cast<std::uint64_t>(slot);  // seed 0 stands for the clock; slots then differ
+  // the ids are read from pageable host memory before the copy call returns; the copy is ordered
+  // on `st` after the slot's earlier picks and accepts, and before the admit kernel
+  if (len > 0 && !hip_ok(hipMemcpyAsync(s->hist + static_cast<size_t>(slot) * s->cap, prompt + (m - len),
+                                        sizeof(int) * static_cast<size_t>(len), hipMemcpyHostToDevice, st),
+                         "copy prompt ids"))
+    return -1;
+  vsmp::launch_slot_admit(s->params, s->rng, s->len, slot, p, rs[0], rs[1], len, st);
+  return hip_ok(hipGetLastError(), "admit launch") ? 0 : -1;
+}
+
+int vsmp_bsampler_pick_rows(vsmp_bsampler* s, const float* logits, int V, long long ld, const int* rows, int n_rows,
+                            int* out, void* stream) {
+  vsmp::clear_error();
+  if (!s) return vsmp::set_error("vsmp: null sampler");
+  if (n_rows < 0 || n_rows > s->n || (n_rows > 0 && !rows))
+    return vsmp::set_error("vsmp: need 0 <= n_rows <= the sampler's slots, and the slot list");
+  if (n_rows == 0) return 0;
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok()) return -1;
+  return vsmp::pick_batch(s->ctx, logits, n_rows, V, ld, s->params, 1, s->hist, s->off, VSMP_U_XORSHIFT, nullptr, s->rng,
+                          0, out, nullptr, static_cast<hipStream_t>(stream), s->len, rows);
+}
+
+int vsmp_bsampler_accept_rows(vsmp_bsampler* s, const int* ids, const int* rows, const int* active, int n_rows,
+                              void* stream) {
+  vsmp::clear_error();
+  if (!s || n_rows < 0 || n_rows > s->n || (n_rows > 0 && (!ids || !rows)))
+    return vsmp::set_error("vsmp: bad accept arguments");
+  if (n_rows == 0) return 0;
+  vsmp::DeviceScope scope(s->device);
+  if (!scope.ok()) return -1;
+  vsmp::launch_hist_accept(s->hist, s->off, s->len, s->cap, s->params, vsmp_params{}, ids, 0, active, rows, n_rows,
+                           s->full, static_cast<hipStream_t>(stream));
   return hip_ok(hipGetLastError(), "accept launch") ? 0 : -1;
 }
 

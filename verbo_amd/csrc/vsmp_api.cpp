@@ -328,9 +328,11 @@ int check_batch(const float* logits, int B, int V, long long ld, const vsmp_para
 // The kernels' arguments that do not depend on the plan or the scratch.
 KArgs batch_args(const float* logits, int B, int V, long long ld, const vsmp_params* params, int params_per_row,
                  const int* hist, const int* hist_off, int u_mode, const double* u, unsigned long long* rng_state,
-                 unsigned long long counter, int* out, const vsmp_debug* dbg, const int* hist_len = nullptr) {
+                 unsigned long long counter, int* out, const vsmp_debug* dbg, const int* hist_len = nullptr,
+                 const int* slot = nullptr) {
   KArgs a{};
   a.hist_len = hist_len;
+  a.slot = slot;
   a.logits = logits;
   a.ld = ld;
   a.B = B;
@@ -365,10 +367,10 @@ KArgs batch_args(const float* logits, int B, int V, long long ld, const vsmp_par
 int launch_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
                  int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
                  unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
-                 hipStream_t st, const int* hist_len) {
+                 hipStream_t st, const int* hist_len, const int* slot) {
   if (check_batch(logits, B, V, ld, params, hist, hist_off, u_mode, u, rng_state, out, dbg) != 0) return -1;
   KArgs a = batch_args(logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter, out, dbg,
-                       hist_len);
+                       hist_len, slot);
   const Plan pl = plan(ctx, B, V, params_per_row ? nullptr : params);
   const size_t slots = static_cast<size_t>(B) * static_cast<size_t>(pl.S);
   if (slots > static_cast<size_t>(INT32_MAX) / kKmax) return set_error("vsmp: batch too large");
@@ -481,11 +483,11 @@ bool after_host_pick(vsmp_ctx* ctx, hipStream_t st) {
 int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
                int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
                unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
-               hipStream_t st, const int* hist_len) {
+               hipStream_t st, const int* hist_len, const int* slot) {
   if (!ctx) return set_error("vsmp: null context");
   if (!after_host_pick(ctx, st)) return -1;
   return launch_batch(ctx, logits, B, V, ld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter, out,
-                      dbg, st, hist_len);
+                      dbg, st, hist_len, slot);
 }
 
 namespace {
@@ -583,7 +585,7 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
     launch_head_gemm(h, head_tile(B, false), st);
     if (!hip_ok(hipGetLastError(), "head launch")) return -1;
     return launch_batch(ctx, full, B, V, fld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
-                        out, dbg, st, nullptr);
+                        out, dbg, st, nullptr, nullptr);
   }
   const int n0 = std::min(kHeadProbe, V);
   const int tile = head_tile(B, false);

@@ -34,6 +34,8 @@ struct KArgs {
   const int* hist;
   const int* hist_off;
   const int* hist_len;  // null: row r's history ends at hist_off[r + 1]; else at hist_off[r] + hist_len[r]
+  const int* slot;      // null: row r is its own sequence; else row r's parameters (when per row), history
+                        // (hist_off / hist_len entries) and draw stream are those of sequence slot[r]
   int u_mode;
   const double* u;
   unsigned long long* rng;
@@ -160,12 +162,17 @@ void launch_head_bound(const KArgs& a, const HeadArgs& h, const float* probe, lo
 void launch_head_finish(const KArgs& a, const HeadArgs& h, hipStream_t st);
 
 // Sampler::accept (reference src/sampler.cpp:43-48) on device-resident histories: row r's history is
-// hist[off[r], off[r] + len[r]) in a region of `cap` ids. For each of the n rows that is active
-// (active null: every row), the id ids[r] (ids null: `tok`) is appended; with repeat_last > 0 a
-// history that would exceed 4 * repeat_last keeps its last repeat_last ids, as the reference trims.
-// A row whose region is full (repeat_last <= 0) appends nothing and sets *full (when not null).
+// hist[off[r], off[r] + len[r]) in a region of `cap` ids. For each of the n entries i that is active
+// (active[i]; active null: every entry), the id ids[i] (ids null: `tok`) is appended to row
+// slots[i] (slots null: row i); with repeat_last > 0 a history that would exceed 4 * repeat_last
+// keeps its last repeat_last ids, as the reference trims. A row whose region is full
+// (repeat_last <= 0) appends nothing and sets *full (when not null).
 void launch_hist_accept(int* hist, const int* off, int* len, int cap, const vsmp_params* params,
-                        const vsmp_params& shared, const int* ids, int tok, const int* active, int n, int* full,
-                        hipStream_t st);
+                        const vsmp_params& shared, const int* ids, int tok, const int* active, const int* slots, int n,
+                        int* full, hipStream_t st);
+// A batched decoder's slot given to a new sequence: params[slot] = p, its xorshift state {s0, s1}
+// and history length h, on `st`.
+void launch_slot_admit(vsmp_params* params, unsigned long long* rng, int* len, int slot, const vsmp_params& p,
+                       unsigned long long s0, unsigned long long s1, int h, hipStream_t st);
 
 }  // namespace vsmp

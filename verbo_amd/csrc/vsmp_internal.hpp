@@ -46,11 +46,13 @@ class DeviceScope {
 
 // One batched pick: the work of vsmp_pick_batch. hist_len (device-resident decode loops): row r's
 // history is hist[hist_off[r], hist_off[r] + hist_len[r]) instead of ending at hist_off[r + 1], so
-// that each row may own a region larger than its history. Returns 0 or -1 (error set).
+// that each row may own a region larger than its history. slot (device, B distinct entries): row r
+// (logits row r, out[r]) samples for sequence slot[r], whose parameters (per row), history entries
+// and draw stream it uses. Returns 0 or -1 (error set).
 int pick_batch(vsmp_ctx* ctx, const float* logits, int B, int V, long long ld, const vsmp_params* params,
                int params_per_row, const int* hist, const int* hist_off, int u_mode, const double* u,
                unsigned long long* rng_state, unsigned long long counter, int* out, const vsmp_debug* dbg,
-               hipStream_t st, const int* hist_len = nullptr);
+               hipStream_t st, const int* hist_len = nullptr, const int* slot = nullptr);
 
 // verbo::Sampler's seeding (reference src/sampler.cpp:11-16,26-31): two successive SplitMix64
 // outputs of the seed; seed 0 stands for the steady clock in microseconds.

@@ -75,8 +75,21 @@ __device__ __forceinline__ double numer(float v, float mx, float temp) {
   return exp(static_cast<double>(v - mx) / static_cast<double>(temp));
 }
 
+// The sequence state of a row (its parameters when per row, its history, its draw stream) is that
+// of slot[row] when the call names slots (a batched decoder's live rows), else of the row itself.
+__device__ __forceinline__ int slot_of(const KArgs& a, int row) { return a.slot ? a.slot[row] : row; }
 __device__ __forceinline__ vsmp_params row_params(const KArgs& a, int row) {
-  return a.params ? a.params[row] : a.shared;
+  return a.params ? a.params[slot_of(a, row)] : a.shared;
+}
+// The row's history: hist[h0, h1) (CSR offsets, or an offset and a length per slot).
+__device__ __forceinline__ void row_hist(const KArgs& a, int row, int& h0, int& h1) {
+  h0 = 0;
+  h1 = 0;
+  if (a.hist_off) {
+    const int s = slot_of(a, row);
+    h0 = a.hist_off[s];
+    h1 = a.hist_len ? h0 + a.hist_len[s] : a.hist_off[s + 1];
+  }
 }
 __device__ __forceinline__ int top_k_of(const vsmp_params& p, int V) {
   return (p.top_k > 0 && p.top_k < V) ? p.top_k : V;  // src/sampler.cpp:72-78
@@ -105,12 +118,13 @@ __device__ __forceinline__ double draw_u(const KArgs& a, int row, const vsmp_par
     return static_cast<double>(z >> 11) * kTwoM53;
   }
   // xorshift128+, src/sampler.cpp:33-41
-  uint64_t s1 = a.rng[2 * row];
-  const uint64_t s0 = a.rng[2 * row + 1];
+  unsigned long long* st = a.rng + 2 * static_cast<size_t>(slot_of(a, row));
+  uint64_t s1 = st[0];
+  const uint64_t s0 = st[1];
   const uint64_t r = s0 + s1;
-  a.rng[2 * row] = s0;
+  st[0] = s0;
   s1 ^= s1 << 23;
-  a.rng[2 * row + 1] = s1 ^ s0 ^ (s1 >> 18) ^ (s0 >> 5);
+  st[1] = s1 ^ s0 ^ (s1 >> 18) ^ (s0 >> 5);
   return static_cast<double>(r >> 11) * kTwoM53;
 }
 
@@ -802,11 +816,8 @@ __global__ __launch_bounds__(kTpb) void k_stage1(KArgs a) {
   const vsmp_params P = row_params(a, row);
   const int path = path_of(P, V, a.smallk_ok);
   const int mode = path == kPathSmallK ? kModeSmallK : (path == kPathGreedy ? kModeBest : kModeBestMin);
-  int h0 = 0, h1 = 0;
-  if (a.hist_off) {
-    h0 = a.hist_off[row];
-    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
-  }
+  int h0, h1;
+  row_hist(a, row, h0, h1);
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
   const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
@@ -1686,7 +1697,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     int base = 0;
     for (int r0 = 0; r0 < a.B; r0 += kGenThreads) {
       const int r = r0 + tid;
-      const bool gen = r < a.B && path_of(a.params[r], V, a.smallk_ok) == kPathGeneral;
+      const bool gen = r < a.B && path_of(row_params(a, r), V, a.smallk_ok) == kPathGeneral;
       double em;
       uint32_t ec;
       block_excl_scan<kGenThreads>(0.0, gen ? 1u : 0u, em, ec, sh.wm, sh.wc);
@@ -1705,11 +1716,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   const int S = a.S;
   exp_tab_fill();  // ordered before its first use by the barriers of the reductions below
 
-  int h0 = 0, h1 = 0;
-  if (a.hist_off) {
-    h0 = a.hist_off[row];
-    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
-  }
+  int h0, h1;
+  row_hist(a, row, h0, h1);
   GenCtx g;
   g.R.rp = a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld);
   g.R.V = V;
@@ -2516,11 +2524,8 @@ __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
     for (int q = 0; q < nmarked; ++q) {
       const int row = list[q];
       const vsmp_params P = row_params(a, row);
-      int h0 = 0, h1 = 0;
-      if (a.hist_off) {
-        h0 = a.hist_off[row];
-        h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
-      }
+      int h0, h1;
+      row_hist(a, row, h0, h1);
       GenRow R;
       R.rp = a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld);
       R.V = V;
@@ -2999,11 +3004,8 @@ __global__ __launch_bounds__(kRowNT) void k_rows(KArgs a) {
   const int nfull = V / (kRowU * 256);           // chunks whose every element lies inside the row
 
   // -- history window (scalar-loaded offsets; ids loaded before the slice)
-  int h0 = 0, h1 = 0;
-  if (a.hist_off) {
-    h0 = a.hist_off[row];
-    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
-  }
+  int h0, h1;
+  row_hist(a, row, h0, h1);
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
   const bool inline_pen = pen && !(P.repeat >= 1.0f);  // repeat < 1 raises values: penalise in the stream
@@ -3351,11 +3353,8 @@ __global__ __launch_bounds__(kTkNT) void k_topk_split(KArgs a) {
   const int ks = min(top_k_of(P, V), max(0, hi - lo));
   const size_t slot = static_cast<size_t>(row) * a.P + part;
 
-  int h0 = 0, h1 = 0;
-  if (a.hist_off) {
-    h0 = a.hist_off[row];
-    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
-  }
+  int h0, h1;
+  row_hist(a, row, h0, h1);
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
   const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
@@ -3655,11 +3654,8 @@ __global__ __launch_bounds__(kSplitNT) void k_greedy_split(KArgs a) {
   const int V4 = (V + 3) >> 2;
   const int G = (V4 + a.P - 1) / a.P;
   const int g0 = min(V4, part * G), g1 = min(V4, g0 + G);
-  int h0 = 0, h1 = 0;
-  if (a.hist_off) {
-    h0 = a.hist_off[row];
-    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
-  }
+  int h0, h1;
+  row_hist(a, row, h0, h1);
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
   const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
@@ -3721,11 +3717,12 @@ __global__ __launch_bounds__(256) void k_read_probe(const uint4* __restrict__ p,
 __global__ __launch_bounds__(256) void k_hist_accept(int* __restrict__ hist, const int* __restrict__ off,
                                                      int* __restrict__ len, int cap, const vsmp_params* params,
                                                      vsmp_params shared, const int* ids, int tok,
-                                                     const int* active, int n, int* full) {
-  const int r = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
-  if (r >= n || (active && !active[r])) return;
+                                                     const int* active, const int* slots, int n, int* full) {
+  const int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (i >= n || (active && !active[i])) return;
+  const int r = slots ? slots[i] : i;  // the sequence entry i appends to
   const vsmp_params P = params ? params[r] : shared;
-  const int t = ids ? ids[r] : tok;
+  const int t = ids ? ids[i] : tok;
   int* h = hist + off[r];
   const int s = len[r];
   const int keep = P.repeat_last > 0 ? P.repeat_last : 0;
@@ -3851,11 +3848,8 @@ __global__ __launch_bounds__(kHbNT) void k_head_bound(KArgs a, HeadArgs h, const
     return;
   }
   // -- history bitmap of the probe columns (src/sampler.cpp:53-65)
-  int h0 = 0, h1 = 0;
-  if (a.hist_off) {
-    h0 = a.hist_off[row];
-    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
-  }
+  int h0, h1;
+  row_hist(a, row, h0, h1);
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
   const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
@@ -3997,11 +3991,8 @@ __global__ __launch_bounds__(kHfNT) void k_head_finish(KArgs a, HeadArgs h) {
   const int V = a.V;
   const int path = path_of(P, V, 1);
   if (path == kPathGeneral) return;
-  int h0 = 0, h1 = 0;
-  if (a.hist_off) {
-    h0 = a.hist_off[row];
-    h1 = a.hist_len ? h0 + a.hist_len[row] : a.hist_off[row + 1];
-  }
+  int h0, h1;
+  row_hist(a, row, h0, h1);
   const int H = h1 - h0;
   const bool pen = (P.repeat != 1.0f) && H > 0;
   const int hfrom = h0 + ((P.repeat_last > 0 && H > P.repeat_last) ? H - P.repeat_last : 0);
@@ -4127,10 +4118,28 @@ void launch_exp_probe(const double* x, double* y, long long n, hipStream_t st) {
 }
 
 void launch_hist_accept(int* hist, const int* off, int* len, int cap, const vsmp_params* params,
-                        const vsmp_params& shared, const int* ids, int tok, const int* active, int n, int* full,
-                        hipStream_t st) {
+                        const vsmp_params& shared, const int* ids, int tok, const int* active, const int* slots, int n,
+                        int* full, hipStream_t st) {
   hipLaunchKernelGGL(k_hist_accept, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, hist, off, len, cap,
-                     params, shared, ids, tok, active, n, full);
+                     params, shared, ids, tok, active, slots, n, full);
+}
+
+// A batched decoder's slot taken by a new sequence (stream-ordered with its picks and accepts): the
+// sequence's parameters, its draw stream's state (seeded on the host) and its history length (the
+// ids themselves are copied before this kernel, on the same stream).
+__global__ void k_slot_admit(vsmp_params* __restrict__ params, unsigned long long* __restrict__ rng,
+                             int* __restrict__ len, int slot, vsmp_params p, unsigned long long s0,
+                             unsigned long long s1, int h) {
+  if (threadIdx.x != 0) return;
+  params[slot] = p;
+  rng[2 * static_cast<size_t>(slot)] = s0;
+  rng[2 * static_cast<size_t>(slot) + 1] = s1;
+  len[slot] = h;
+}
+
+void launch_slot_admit(vsmp_params* params, unsigned long long* rng, int* len, int slot, const vsmp_params& p,
+                       unsigned long long s0, unsigned long long s1, int h, hipStream_t st) {
+  hipLaunchKernelGGL(k_slot_admit, dim3(1), dim3(64), 0, st, params, rng, len, slot, p, s0, s1, h);
 }
 
 void launch_zero_u32(uint32_t* p, long long n, hipStream_t st) {

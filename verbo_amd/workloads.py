@@ -249,3 +249,48 @@ class DecodeCase:
                 v[0] += 6.0
             x[r] = v.astype(np.float32)
         return x
+
+
+class ServeCase:
+    """A seeded request stream for a continuous-batching server: R requests arriving over time at a
+    batched decoder of `slots` slots (fewer than R, so finished sequences' slots are taken again).
+    Each request has the fields of verbo_gen_opts plus repeat_last, a prompt and an arrival step;
+    its next-position logits depend only on the request, its own step (steps since it was
+    admitted) and its last id, so a request decodes the same whatever else shares the batch. Id 0
+    is the stop id; from its own step stop_after[j] on it gets a large bonus. A few requests ask for
+    no tokens at all, and bursts arrive together, so some wait in the queue for a free slot."""
+
+    def __init__(self, n=40, slots=8, V=4096, seed=0x70):
+        self.n, self.slots, self.V, self.seed = n, slots, V, seed
+        u = uniform(seed, 0, 10 * n).reshape(n, 10)
+        self.opts, self.repeat_last, self.prompts, self.stop_after, self.arrival = [], [], [], [], []
+        for j in range(n):
+            mt = 4 + int(u[j, 0] * 30)
+            if j % 13 == 5:
+                mt = 0  # asks for nothing: finishes at once, takes no slot
+            self.opts.append(dict(max_tokens=mt,
+                                  temp=(0.0, 0.5, 0.8, 1.2)[int(u[j, 1] * 4)],
+                                  top_k=(0, 20, 40, 300)[int(u[j, 2] * 4)],
+                                  top_p=(0.8, 0.95, 1.0)[int(u[j, 3] * 3)],
+                                  min_p=(0.0, 0.05)[int(u[j, 4] * 2)],
+                                  repeat=(1.0, 1.15, 1.3)[int(u[j, 5] * 3)],
+                                  seed=500 + j))
+            self.repeat_last.append((4, 16, 64)[j % 3])
+            self.prompts.append(_ints(seed + 1, j * 64, 1 + int(u[j, 6] * 40), 1, V).astype(np.int32))
+            self.stop_after.append(3 + int(u[j, 7] * 30))
+            # bursts: a third of the requests arrive at step 0, the others spread over 60 steps
+            self.arrival.append(0 if u[j, 8] < 1 / 3 else int(u[j, 9] * 60))
+        self.stop_ids = (0,)
+
+    def logits(self, reqs, steps, last):
+        """Logits [len(reqs), V] (fp32): row i is request reqs[i]'s next position at its own step
+        steps[i], after its last id last[i] (-1 before its first pick)."""
+        x = np.empty((len(reqs), self.V), np.float32)
+        for i, (j, t, l) in enumerate(zip(reqs, steps, last)):
+            v = 2.0 * normal(self.seed + 2 + j, int(t) * self.V, self.V)
+            if l >= 0:
+                v[(int(l) * 7 + 13) % self.V] += 3.0
+            if t >= self.stop_after[j]:
+                v[0] += 6.0
+            x[i] = v.astype(np.float32)
+        return x
