@@ -50,3 +50,24 @@ def test_reference_test_binary_on_the_gpu_sampler(tmp_path):
     lines = [x.strip() for x in out.splitlines()]
     for group in ("sampler", "generate", "capi"):
         assert lines[lines.index(group) + 1] == "ok", group
+
+
+def test_verbo_cli_run_through_the_swapped_build():
+    """verbo's own command line (`verbo run`, reference cli/main.cpp:39-66, generate at :58) linked
+    against the GPU sampler prints what the unswapped build printed (tests/golden/cli_run_golden.jsonl,
+    recorded by tests/golden/make_cli_golden.py), byte for byte: greedy, top-k, top-p only, min-p with
+    penalties, raw text and the chat template, q8 and f32 models."""
+    import base64
+    import sys
+
+    sys.path.insert(0, str(ROOT / "tests" / "golden"))
+    from make_cli_golden import command
+
+    exe = SWAP / "verbo"
+    _need(exe)
+    gold = [json.loads(x) for x in (ROOT / "tests" / "golden" / "cli_run_golden.jsonl").read_text().splitlines()]
+    assert len(gold) >= 6
+    for g in gold:
+        print("swapped verbo run:", g["name"], flush=True)
+        out = subprocess.run(command(exe, g["model"], g["args"]), check=True, capture_output=True, timeout=120).stdout
+        assert out == base64.b64decode(g["stdout_b64"]), (g["name"], out)
