@@ -253,15 +253,18 @@ __global__ __launch_bounds__(64 * WM * WN) void k_head_gemm(HeadArgs h) {
 struct TileShape {
   int rows, cols;
 };
-// 0..3: main products (B > 128, > 64, > 32, <= 32); 4, 5: probe products (narrow tiles, so that
-// many workgroups share the few probe columns: B > 32, B <= 32)
-constexpr TileShape kTiles[] = {{256, 128}, {128, 128}, {64, 128}, {32, 128}, {64, 32}, {32, 32}};
+// 6, 1, 2, 3: main products (B > 128, > 64, > 32, <= 32); 4, 5: probe products (narrow tiles, so
+// that many workgroups share the few probe columns: B > 32, B <= 32); 0 is not routed to. Over 128
+// rows each wave of the 256 x 256 tile owns 64 x 128 (two register stages of loads in flight, 236
+// VGPRs, one workgroup per CU): at 256 x 151,936 x 896, 110 against 116.6 us for 256 x 128 tiles
+// (64 x 64 per wave), whose LDS reads per chunk (128 KB) outweigh their MFMA work.
+constexpr TileShape kTiles[] = {{256, 128}, {128, 128}, {64, 128}, {32, 128}, {64, 32}, {32, 32}, {256, 256}};
 
 }  // namespace
 
 int head_tile(int B, bool probe) {
   if (probe) return B > 32 ? 4 : 5;
-  if (B > 128) return 0;
+  if (B > 128) return 6;
   if (B > 64) return 1;
   return B > 32 ? 2 : 3;
 }
@@ -277,6 +280,7 @@ void launch_head_gemm(const HeadArgs& h, int tile, hipStream_t st) {
     case 2: hipLaunchKernelGGL((k_head_gemm<1, 1, 2, 4, 4>), grid, dim3(512), 0, st, h); break;
     case 3: hipLaunchKernelGGL((k_head_gemm<1, 1, 1, 4, 4>), grid, dim3(256), 0, st, h); break;
     case 4: hipLaunchKernelGGL((k_head_gemm<1, 1, 2, 1, 4>), grid, dim3(128), 0, st, h); break;
+    case 6: hipLaunchKernelGGL((k_head_gemm<2, 4, 4, 2, 2>), grid, dim3(512), 0, st, h); break;
     default: hipLaunchKernelGGL((k_head_gemm<1, 1, 1, 1, 4>), grid, dim3(64), 0, st, h); break;
   }
 }
