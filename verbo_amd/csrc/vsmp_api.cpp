@@ -536,7 +536,7 @@ int head_logits(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* he
   h.col1 = V;
   h.out = logits;
   h.ldo = ldl;
-  launch_head_gemm(h, head_tile(B, false), st);
+  launch_head_gemm(h, head_tile(B, false), ctx->cus, st);
   return hip_ok(hipGetLastError(), "head launch") ? 0 : -1;
 }
 
@@ -582,7 +582,7 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
     h.col1 = V;
     h.out = full;
     h.ldo = fld;
-    launch_head_gemm(h, head_tile(B, false), st);
+    launch_head_gemm(h, head_tile(B, false), ctx->cus, st);
     if (!hip_ok(hipGetLastError(), "head launch")) return -1;
     return launch_batch(ctx, full, B, V, fld, params, params_per_row, hist, hist_off, u_mode, u, rng_state, counter,
                         out, dbg, st, nullptr, nullptr);
@@ -614,7 +614,7 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
   hp.col1 = n0;
   hp.out = probe;
   hp.ldo = pld;
-  launch_head_gemm(hp, head_tile(B, true), st);
+  launch_head_gemm(hp, head_tile(B, true), 0, st);
   if (!hip_ok(hipGetLastError(), "probe launch")) return -1;
   // 2. per row: the bound, the mode and the probe's candidates
   h.tk = ctx->h_tk;
@@ -631,7 +631,7 @@ int head_pick(vsmp_ctx* ctx, const void* hidden, long long ldh, const void* head
     hm.col1 = V;
     hm.out = full;
     hm.ldo = fld;
-    launch_head_gemm(hm, tile, st);
+    launch_head_gemm(hm, tile, ctx->cus, st);
     if (!hip_ok(hipGetLastError(), "head launch")) return -1;
   }
   // 4. greedy and small-k rows: the exact top-k and the epilogue

@@ -152,7 +152,9 @@ struct HeadArgs {
 int head_tile(int B, bool probe);
 int head_tile_cols(int tile);
 int head_tile_rows(int tile);
-void launch_head_gemm(const HeadArgs& h, int tile, hipStream_t st);
+// The head's product over columns [h.col0, h.col1) on tiles of shape `tile`; cus: the device's CUs,
+// by which the widest tile's last, partial round is cut into narrower tiles (0: no cut).
+void launch_head_gemm(const HeadArgs& h, int tile, int cus, hipStream_t st);
 // Per row, after the probe product: the bound tk (from the probe's penalised logits, src/sampler.cpp
 // semantics), the row's mode and its first candidates (those of the probe columns).
 void launch_head_bound(const KArgs& a, const HeadArgs& h, const float* probe, long long pld, int n0, int write_all,
