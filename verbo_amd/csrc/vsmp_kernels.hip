@@ -3613,6 +3613,18 @@ __device__ __forceinline__ uint64_t greedy_part(const KArgs& a, int row, int g0,
     __syncthreads();
   }
 
+  // The penalty nibbles of the thread's eight groups (group d of the part: word d >> 3, bits
+  // 4d % 32), read from LDS together before any of the part's loads is waited for. A group past g1
+  // reads a word of the array that may be stale; its nibble is never used.
+  uint32_t nibs = 0u;
+  if (PEN) {
+#pragma unroll
+    for (int u = 0; u < kSplitU; ++u) {
+      const int d = u * kSplitNT + tid;
+      nibs |= ((bits[d >> 3] >> ((4 * d) & 31)) & 0xFu) << (4 * u);
+    }
+  }
+
   // per thread in increasing index order (strictly larger keys only: the first maximum stays)
   uint32_t bk = 0u;
   int bi = 0;
@@ -3623,7 +3635,7 @@ __device__ __forceinline__ uint64_t greedy_part(const KArgs& a, int row, int g0,
     const int e = 4 * f;
     float x[4] = {__uint_as_float(v[u].x), __uint_as_float(v[u].y), __uint_as_float(v[u].z), __uint_as_float(v[u].w)};
     if (PEN) {
-      const uint32_t nib = (bits[(e - lo) >> 5] >> ((e - lo) & 31)) & 0xFu;
+      const uint32_t nib = (nibs >> (4 * u)) & 0xFu;
       if (nib) {
 #pragma unroll
         for (int c = 0; c < 4; ++c)
@@ -3639,7 +3651,14 @@ __device__ __forceinline__ uint64_t greedy_part(const KArgs& a, int row, int g0,
       }
     }
   }
-  return block_max64<kSplitNT>(bk ? comp(bk, static_cast<uint32_t>(bi)) : 0ull, red64);
+  // the part's maximum: each wave's by DPP, then one barrier (red64 has no earlier use here)
+  const uint64_t wm = wave_max_u64(bk ? comp(bk, static_cast<uint32_t>(bi)) : 0ull);
+  if ((tid & 63) == 0) red64[tid >> 6] = wm;
+  __syncthreads();
+  uint64_t r = red64[0];
+#pragma unroll
+  for (int i = 1; i < kSplitNT / 64; ++i) r = max64(r, red64[i]);
+  return r;
 }
 
 __global__ __launch_bounds__(kSplitNT) void k_greedy_split(KArgs a) {
@@ -3669,7 +3688,7 @@ __global__ __launch_bounds__(kSplitNT) void k_greedy_split(KArgs a) {
     for (int i = tid; i < words; i += kSplitNT) np += __popc(bits[i]);
     np = block_sum_u32<kSplitNT>(np, red32);
   }
-  if (a.pen_bits && pen) or_pen_ids<kSplitNT>(a, row, lo, bits, words);  // bits: complete (block_max64's barriers)
+  if (a.pen_bits && pen) or_pen_ids<kSplitNT>(a, row, lo, bits, words);  // bits: complete (the bitmap's barrier)
   if (tid == 0) {
     __hip_atomic_fetch_max(&a.g_slot[row], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (a.info) __hip_atomic_fetch_add(&a.g_npen[row], np, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
