@@ -69,12 +69,16 @@ def test_head_logits_match_fp32_product(ctx, B, Vv, D):
     assert (err <= 2e-5 * mag + 1e-30).all(), float(np.max(err / np.maximum(mag, 1e-30)))
 
 
-def test_head_logits_do_not_depend_on_the_batch(ctx):
+@pytest.mark.parametrize("D", [320, 896])
+def test_head_logits_do_not_depend_on_the_batch(ctx, D):
     """A row's logits are the same bits whether it is computed alone, in a batch of 77 or of 256
-    (different tile shapes), and whether vsmp_head_pick writes them or vsmp_head_logits does."""
+    (different tile shapes; at D = 896 the 256-row batch takes the four-wave tile with the
+    hidden block in LDS by direct loads), and whether vsmp_head_pick writes them or
+    vsmp_head_logits does."""
     import torch
 
-    hidden, head = operands(5, 256, 12345, 320)
+    log("head logits across tiles", D)
+    hidden, head = operands(5, 256, 12345, D)
     full = ctx.head_logits(hidden, head)
     mid = ctx.head_logits(hidden[:77].contiguous(), head)
     one = ctx.head_logits(hidden[200:201].contiguous(), head)
