@@ -486,7 +486,8 @@ def test_greedy_split_parts(dmode):
     """Greedy batches cut into parts (one launch, the last part of a row writes its id) against the
     oracle and against one workgroup per row: ties of the maximum in different parts (the lowest
     index wins), the maximum itself penalised, parts that end inside a 16-byte group or hold no
-    group, consecutive calls reusing the per-row slots, and a call without diagnostics."""
+    group, consecutive calls reusing the per-row slots, and calls without diagnostics (which fold
+    the parts' maxima through one compare-and-swap word per row: two calls in a row at every shape)."""
     import torch
 
     ctx = mode_ctx(dmode)
@@ -506,11 +507,14 @@ def test_greedy_split_parts(dmode):
         for r in range(B):
             hh = np.asarray(hists[r])
             assert run.info["n_pen"][r] == len(np.unique(hh[(hh >= 0) & (hh < Vv)])), r
-    d = torch.from_numpy(lg).cuda()
-    pr = V.Params(*[p[0][f].item() for f in V.SAMPLING_DTYPE.names])
-    out = ctx.pick_batch(d, pr, torch.from_numpy(h).cuda(), torch.from_numpy(off).cuda())
-    torch.cuda.synchronize()
-    assert (out.cpu().numpy() == run.o_ids).all()
+        buf = torch.zeros((B, (Vv + 3) // 4 * 4), dtype=torch.float32)  # rows padded to a multiple of 4
+        buf[:, :Vv] = torch.from_numpy(lg)
+        d = buf.cuda()[:, :Vv]
+        pr = V.Params(*[p[0][f].item() for f in V.SAMPLING_DTYPE.names])
+        for _ in range(2):
+            out = ctx.pick_batch(d, pr, torch.from_numpy(h).cuda(), torch.from_numpy(off).cuda())
+            torch.cuda.synchronize()
+            assert (out.cpu().numpy() == run.o_ids).all(), (B, Vv)
 
 
 def test_vocabulary_beyond_the_row_kernel(ctx):
