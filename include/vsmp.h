@@ -11,6 +11,10 @@
  * read with vsmp_last_error(). Device pointers are plain HIP device addresses; `stream` is a
  * hipStream_t (NULL = the default stream). Batched calls are stream-ordered and do not
  * synchronise the host.
+ *
+ * Logits are finite fp32 values or -inf. +inf and NaN are not supported: they are outside the
+ * reference's defined behaviour too (with +inf its numerator exp(float(v - mx) / temp) is NaN, and
+ * NaN breaks its sort's ordering). The library does not scan the logits for them.
  */
 #ifndef VSMP_H
 #define VSMP_H
