@@ -53,7 +53,7 @@ def fp32_reference(hidden, head):
 
 
 @pytest.mark.parametrize("B,Vv,D", [(1, 1000, 64), (37, 4099, 128), (130, 5000, 192), (64, 8269, 256),
-                                    (256, 20000, 896), (8, 5000, 4096)])
+                                    (256, 20000, 896), (8, 5000, 4096), (200, 151936, 896)])
 def test_head_logits_match_fp32_product(ctx, B, Vv, D):
     """Every logit within 2e-5 of sum |x_d w_d| of the fp32 product: the fp32 accumulation of D
     exact bf16 products in another order (and one that swaps rows or columns is off by far more)."""
@@ -69,26 +69,27 @@ def test_head_logits_match_fp32_product(ctx, B, Vv, D):
     assert (err <= 2e-5 * mag + 1e-30).all(), float(np.max(err / np.maximum(mag, 1e-30)))
 
 
-@pytest.mark.parametrize("D", [320, 896])
-def test_head_logits_do_not_depend_on_the_batch(ctx, D):
+@pytest.mark.parametrize("Vv,D", [(12345, 320), (12345, 896), (151936, 896)])
+def test_head_logits_do_not_depend_on_the_batch(ctx, Vv, D):
     """A row's logits are the same bits whether it is computed alone, in a batch of 77 or of 256
-    (different tile shapes; at D = 896 the 256-row batch takes the four-wave tile with the
-    hidden block in LDS by direct loads), and whether vsmp_head_pick writes them or
-    vsmp_head_logits does."""
+    (different tile shapes; at 151,936 columns the 256-row batch's product is two launches, the
+    columns of the whole rounds on 256 x 256 tiles and the rest on 256 x 128 tiles), and whether
+    vsmp_head_pick writes them or vsmp_head_logits does."""
     import torch
 
-    log("head logits across tiles", D)
-    hidden, head = operands(5, 256, 12345, D)
+    log("head logits across tiles", Vv, D)
+    hidden, head = operands(5, 256, Vv, D)
     full = ctx.head_logits(hidden, head)
     mid = ctx.head_logits(hidden[:77].contiguous(), head)
     one = ctx.head_logits(hidden[200:201].contiguous(), head)
-    lg = torch.full((256, 12348), float("nan"), dtype=torch.float32, device="cuda")
+    ldl = (Vv + 3) // 4 * 4
+    lg = torch.full((256, ldl), float("nan"), dtype=torch.float32, device="cuda")
     ctx.head_pick(hidden, head, V.Params(temp=0.8, top_k=50, top_p=0.95, repeat=1.0), logits=lg)
     torch.cuda.synchronize()
     f = full.cpu().numpy()
     assert np.array_equal(mid.cpu().numpy(), f[:77])
     assert np.array_equal(one.cpu().numpy(), f[200:201])
-    assert np.array_equal(lg[:, :12345].cpu().numpy(), f)
+    assert np.array_equal(lg[:, :Vv].cpu().numpy(), f)
 
 
 def head_run(ctx, hidden, head, params, hist=None, hist_off=None, cand_cap=128):
