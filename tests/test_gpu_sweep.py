@@ -9,7 +9,12 @@ general rows with shared parameters run as two 512-thread workgroups per CU).
 The LM head's pick (vsmp_head_pick) takes its own sweep: random bf16 hidden states and heads of 64
 to 896 hidden elements and 1,000 to 151,936 columns, batches of 1 to 257 rows on the route by batch
 size or the fused route pinned, every sampling mode, checked against the oracle on the logits the
-head itself produces."""
+head itself produces.
+
+VSMP_SWEEP_CASES / VSMP_SWEEP_SEED and VSMP_HEAD_SWEEP_CASES / VSMP_HEAD_SWEEP_SEED run longer
+sweeps, or other seeds, of the same generators (defaults 300 / 2024 and 60 / 2025)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -18,7 +23,8 @@ from helpers import Run, csr, log, mode_ctx
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 300
+N_CASES = int(os.environ.get("VSMP_SWEEP_CASES", "300"))
+SEED = int(os.environ.get("VSMP_SWEEP_SEED", "2024"))
 
 
 def case(rng):
@@ -51,7 +57,7 @@ def case(rng):
 
 
 def test_randomised_batches():
-    rng = np.random.default_rng(2024)
+    rng = np.random.default_rng(SEED)
     near = 0
     for i in range(N_CASES):
         desc, lg, p, h, off = case(rng)
@@ -63,7 +69,8 @@ def test_randomised_batches():
     log("sweep:", N_CASES, "cases,", near, "draws within 1e-6 of a CDF boundary, none of them mismatched")
 
 
-N_HEAD_CASES = 60
+N_HEAD_CASES = int(os.environ.get("VSMP_HEAD_SWEEP_CASES", "60"))
+HEAD_SEED = int(os.environ.get("VSMP_HEAD_SWEEP_SEED", "2025"))
 
 
 def head_case(rng):
@@ -96,7 +103,7 @@ def head_case(rng):
 def test_randomised_head_batches():
     import torch
 
-    rng = np.random.default_rng(2025)
+    rng = np.random.default_rng(HEAD_SEED)
     near = 0
     for i in range(N_HEAD_CASES):
         desc, hidden, head, p, h, off = head_case(rng)
