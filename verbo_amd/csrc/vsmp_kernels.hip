@@ -94,9 +94,20 @@ __device__ __forceinline__ void row_hist(const KArgs& a, int row, int& h0, int& 
 __device__ __forceinline__ int top_k_of(const vsmp_params& p, int V) {
   return (p.top_k > 0 && p.top_k < V) ? p.top_k : V;  // src/sampler.cpp:72-78
 }
+__device__ __forceinline__ int path_of_tk(float temp, int top_k, int V, int smallk_ok) {
+  if (temp <= 0.0f) return kPathGreedy;
+  const int k = (top_k > 0 && top_k < V) ? top_k : V;
+  return (smallk_ok && k <= kKmax) ? kPathSmallK : kPathGeneral;
+}
 __device__ __forceinline__ int path_of(const vsmp_params& p, int V, int smallk_ok) {
-  if (p.temp <= 0.0f) return kPathGreedy;
-  return (smallk_ok && top_k_of(p, V) <= kKmax) ? kPathSmallK : kPathGeneral;
+  return path_of_tk(p.temp, p.top_k, V, smallk_ok);
+}
+// The path of a row from the two fields that decide it, read alone (per-lane searches over the
+// batch's rows keep only these in registers).
+__device__ __forceinline__ int row_path(const KArgs& a, int row, int V, int smallk_ok) {
+  if (!a.params) return path_of_tk(a.shared.temp, a.shared.top_k, V, smallk_ok);
+  const vsmp_params* p = a.params + slot_of(a, row);
+  return path_of_tk(p->temp, p->top_k, V, smallk_ok);
 }
 
 // ---- uniform draws ------------------------------------------------------------------------------
@@ -1697,7 +1708,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     int base = 0;
     for (int r0 = 0; r0 < a.B; r0 += kGenThreads) {
       const int r = r0 + tid;
-      const bool gen = r < a.B && path_of(row_params(a, r), V, a.smallk_ok) == kPathGeneral;
+      const bool gen = r < a.B && row_path(a, r, V, a.smallk_ok) == kPathGeneral;
       double em;
       uint32_t ec;
       block_excl_scan<kGenThreads>(0.0, gen ? 1u : 0u, em, ec, sh.wm, sh.wc);
@@ -2486,7 +2497,6 @@ __device__ void exact_flat_row(const KArgs& a, int row, const vsmp_params& P, in
 __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
   __shared__ int list[kGenThreads];
   __shared__ int nlist;
-  __shared__ int wmarked[kGenThreads / 64];
   __shared__ int xkeep;
   __shared__ double xd[8];
   __shared__ int xi[4];
@@ -2497,35 +2507,31 @@ __global__ __launch_bounds__(kGenThreads) void k_general_exact(KArgs a) {
   const int V = a.V, n2 = a.x_n;
   uint64_t* xs = reinterpret_cast<uint64_t*>(a.x_buf) + static_cast<size_t>(blockIdx.x) * 2 * static_cast<size_t>(n2);
   double* pr = reinterpret_cast<double*>(xs + n2);
-  // The marked rows, in row order, are dealt to the workgroups in turn (the m-th to workgroup m mod
-  // grid), so that however few slots the batch has, marked rows are spread evenly over them and no
-  // other row costs more than its flag read.
-  int seen = 0;  // marked rows before this chunk of the batch
-  for (int c0 = 0; c0 < a.B; c0 += kGenThreads) {
+  // Row r goes to workgroup r mod grid: however few slots the batch has, each workgroup reads the
+  // flags of its share of the rows and redoes its marked ones, and no other row costs more than its
+  // flag read. (Dealing the marked rows in turn by a ballot prefix balanced adversarial patterns
+  // better, but its registers made the kernel spill, and a kernel with scratch costs every general
+  // batch about 11 us at 512 x 151936, marked rows or not.)
+  for (int c0 = blockIdx.x; c0 < a.B; c0 += gridDim.x * kGenThreads) {
     if (tid == 0) nlist = 0;
+    __syncthreads();
     {
-      const int r = c0 + tid;
-      const bool m = r < a.B && a.x_flag[r] != 0 && path_of(row_params(a, r), V, a.smallk_ok) == kPathGeneral;
-      const uint64_t bal = __ballot(m);
-      const int lane = tid & 63, w = tid >> 6;
-      if (lane == 0) wmarked[w] = __popcll(bal);
-      __syncthreads();
-      int before = 0, total = 0;
-      for (int i = 0; i < kGenThreads / 64; ++i) {
-        before += i < w ? wmarked[i] : 0;
-        total += wmarked[i];
-      }
-      const int idx = seen + before + __popcll(bal & ((1ull << lane) - 1ull));
-      if (m && idx % static_cast<int>(gridDim.x) == static_cast<int>(blockIdx.x)) list[atomicAdd(&nlist, 1)] = r;
-      seen += total;
+      const int r = c0 + static_cast<int>(gridDim.x) * tid;
+      if (r < a.B && a.x_flag[r] != 0 && row_path(a, r, V, a.smallk_ok) == kPathGeneral)
+        list[atomicAdd(&nlist, 1)] = r;
     }
     __syncthreads();
     const int nmarked = nlist;
     for (int q = 0; q < nmarked; ++q) {
-      const int row = list[q];
-      const vsmp_params P = row_params(a, row);
-      int h0, h1;
-      row_hist(a, row, h0, h1);
+      // the row, its slot, parameters and history window are uniform: read into scalar registers
+      const int row = __builtin_amdgcn_readfirstlane(list[q]);
+      const int sl = __builtin_amdgcn_readfirstlane(slot_of(a, row));
+      const vsmp_params P = a.params ? a.params[sl] : a.shared;
+      int h0 = 0, h1 = 0;
+      if (a.hist_off) {
+        h0 = __builtin_amdgcn_readfirstlane(a.hist_off[sl]);
+        h1 = __builtin_amdgcn_readfirstlane(a.hist_len ? h0 + a.hist_len[sl] : a.hist_off[sl + 1]);
+      }
       GenRow R;
       R.rp = a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld);
       R.V = V;
