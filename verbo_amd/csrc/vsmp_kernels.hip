@@ -75,6 +75,29 @@ __device__ __forceinline__ double numer(float v, float mx, float temp) {
   return exp(static_cast<double>(v - mx) / static_cast<double>(temp));
 }
 
+// A value every lane of the wave holds alike, moved into scalar registers: it then holds no vector
+// register through the passes that follow.
+__device__ __forceinline__ uint32_t sgpr_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+__device__ __forceinline__ uint64_t sgpr_u64(uint64_t v) {
+  return (static_cast<uint64_t>(sgpr_u32(static_cast<uint32_t>(v >> 32))) << 32) | sgpr_u32(static_cast<uint32_t>(v));
+}
+__device__ __forceinline__ double sgpr_f64(double v) { return __longlong_as_double(static_cast<long long>(sgpr_u64(static_cast<uint64_t>(__double_as_longlong(v))))); }
+__device__ __forceinline__ float sgpr_f32(float v) { return __uint_as_float(sgpr_u32(__float_as_uint(v))); }
+__device__ __forceinline__ int sgpr_i32(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// A row's parameters, when every lane of the workgroup takes the same row.
+__device__ __forceinline__ vsmp_params sgpr_params(vsmp_params p) {
+  p.temp = sgpr_f32(p.temp);
+  p.top_k = sgpr_i32(p.top_k);
+  p.top_p = sgpr_f32(p.top_p);
+  p.min_p = sgpr_f32(p.min_p);
+  p.repeat = sgpr_f32(p.repeat);
+  p.repeat_last = sgpr_i32(p.repeat_last);
+  p.seed = sgpr_u64(p.seed);
+  return p;
+}
+
 // The sequence state of a row (its parameters when per row, its history, its draw stream) is that
 // of slot[row] when the call names slots (a batched decoder's live rows), else of the row itself.
 __device__ __forceinline__ int slot_of(const KArgs& a, int row) { return a.slot ? a.slot[row] : row; }
@@ -145,49 +168,49 @@ __device__ __forceinline__ uint64_t max64(uint64_t a, uint64_t b) { return a > b
 __device__ __forceinline__ uint64_t min64(uint64_t a, uint64_t b) { return a < b ? a : b; }
 
 template <int NT>
-__device__ uint64_t block_max64(uint64_t v, uint64_t* red) {
+__device__ __forceinline__ uint64_t block_max64(uint64_t v, uint64_t* red) {
   for (int o = 32; o > 0; o >>= 1) v = max64(v, __shfl_xor(v, o));
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   uint64_t r = red[0];
   for (int i = 1; i < NT / 64; ++i) r = max64(r, red[i]);
-  return r;
+  return sgpr_u64(r);
 }
 template <int NT>
-__device__ uint64_t block_min64(uint64_t v, uint64_t* red) {
+__device__ __forceinline__ uint64_t block_min64(uint64_t v, uint64_t* red) {
   for (int o = 32; o > 0; o >>= 1) v = min64(v, __shfl_xor(v, o));
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   uint64_t r = red[0];
   for (int i = 1; i < NT / 64; ++i) r = min64(r, red[i]);
-  return r;
+  return sgpr_u64(r);
 }
 template <int NT>
-__device__ double block_sum_f64(double v, double* red) {
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   double r = red[0];
   for (int i = 1; i < NT / 64; ++i) r += red[i];
-  return r;
+  return sgpr_f64(r);
 }
 template <int NT>
-__device__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   uint32_t r = red[0];
   for (int i = 1; i < NT / 64; ++i) r += red[i];
-  return r;
+  return sgpr_u32(r);
 }
 
 // Exclusive block scan of one (mass, count) pair per thread; deterministic order.
 template <int NT>
-__device__ void block_excl_scan(double m, uint32_t c, double& em, uint32_t& ec, double* wm, uint32_t* wc) {
+__device__ __forceinline__ void block_excl_scan(double m, uint32_t c, double& em, uint32_t& ec, double* wm, uint32_t* wc) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   double im = m;
@@ -1535,13 +1558,13 @@ __device__ __forceinline__ Sel find_in_prefix(GenShared<NT>& sh, const uint64_t*
     __syncthreads();
     return s;
   }
-  int j = sh.ints[5];
+  int j = sgpr_i32(sh.ints[5]);
   s.found = j < m;
   if (!s.found) j = m - 1;  // rounding left the target just past this range: its last element
-  s.ck = list[j];
+  s.ck = sgpr_u64(list[j]);
   s.rank = rank_above + j;
-  s.before = j > 0 ? lpr[j - 1] : above;
-  s.incl = lpr[j];
+  s.before = j > 0 ? sgpr_f64(lpr[j - 1]) : above;
+  s.incl = sgpr_f64(lpr[j]);
   __syncthreads();
   return s;
 }
@@ -1631,7 +1654,7 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared<NT>& sh,
     }
     wave_claim_min(&sh.ints[0], first >= 0, first);
     __syncthreads();
-    int pos = sh.ints[0];
+    int pos = sgpr_i32(sh.ints[0]);
     if (pos == kRefBuckets) {
       // target not reached (rounding): continue in the last non-empty bucket
       if (tid == 0) sh.ints[1] = -1;
@@ -1642,7 +1665,7 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared<NT>& sh,
         if (cv[r]) last = p0 + r;
       if (last >= 0) atomicMax(&sh.ints[1], last);
       __syncthreads();
-      pos = sh.ints[1];
+      pos = sgpr_i32(sh.ints[1]);
     }
     // owner of `pos` publishes the weight / count before it
     if (pos >= p0 && pos < p0 + RP) {
@@ -1660,9 +1683,9 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared<NT>& sh,
       }
     }
     __syncthreads();
-    above = sh.dbls[0];
-    rank_above = sh.ints[2];
-    n = sh.ints[3];
+    above = sgpr_f64(sh.dbls[0]);
+    rank_above = sgpr_i32(sh.ints[2]);
+    n = sgpr_i32(sh.ints[3]);
     const int d = kRefBuckets - 1 - pos;
     const uint64_t nlo = clo + (static_cast<uint64_t>(d) << shift);
     uint64_t nhi = nlo + ((1ull << shift) - 1ull);
@@ -1686,7 +1709,7 @@ __device__ __forceinline__ Sel refine_select(const GenCtx& g, GenShared<NT>& sh,
   });
   }
   __syncthreads();
-  const int m = min(sh.ints[4], kGenCap);
+  const int m = min(sgpr_i32(sh.ints[4]), kGenCap);
   sort_desc(sh, sh.list, reinterpret_cast<uint64_t*>(sh.lpr), m);
   return scan_sorted<MASS>(g, sh, sh.list, sh.lpr, m, rank_above, above, target);
 }
@@ -1722,13 +1745,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     __syncthreads();
     if (row < 0) return;  // fewer general rows than workgroups
   }
-  const vsmp_params P = row_params(a, row);
+  // the row, so its parameters and history window, are the same in every lane: scalar registers
+  const vsmp_params P = sgpr_params(row_params(a, row));
   if (path_of(P, V, a.smallk_ok) != kPathGeneral) return;
   const int S = a.S;
   exp_tab_fill();  // ordered before its first use by the barriers of the reductions below
 
   int h0, h1;
   row_hist(a, row, h0, h1);
+  h0 = sgpr_i32(h0);
+  h1 = sgpr_i32(h1);
   GenCtx g;
   g.R.rp = a.logits + static_cast<size_t>(row) * static_cast<size_t>(a.ld);
   g.R.V = V;
@@ -1991,7 +2017,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     __syncthreads();
   }
   // the sum over the top-k prefix (src/sampler.cpp:84): the histogram's total
-  const double sum = sh.mass0[kGenBuckets - 1];
+  const double sum = sgpr_f64(sh.mass0[kGenBuckets - 1]);
 
   // src/sampler.cpp:86-91 (min-p), with the count of a prefix
   int keep = k;
@@ -2021,7 +2047,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       wave_claim_min(&sh.ints[6], sh.cnt0[b] > prev && sh.mass0[b] >= target, b);
     }
     __syncthreads();
-    const int qb = sh.ints[6];
+    const int qb = sgpr_i32(sh.ints[6]);
     __syncthreads();
     return qb;
   };
@@ -2044,13 +2070,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       s.found = false;
       s.ck = 0ull;
       s.rank = 0;
-      s.before = s.incl = sh.mass0[kGenBuckets - 1];
+      s.before = s.incl = sum;
       __syncthreads();
       return s;
     }
-    const double above = qb > 0 ? sh.mass0[qb - 1] : 0.0;
-    const int rank_above = qb > 0 ? static_cast<int>(sh.cnt0[qb - 1]) : 0;
-    const int n = static_cast<int>(sh.cnt0[qb]) - rank_above;
+    const double above = qb > 0 ? sgpr_f64(sh.mass0[qb - 1]) : 0.0;
+    const int rank_above = qb > 0 ? sgpr_i32(static_cast<int>(sh.cnt0[qb - 1])) : 0;
+    const int n = sgpr_i32(static_cast<int>(sh.cnt0[qb])) - rank_above;
     const uint64_t ckk = g.ckk;
     auto in_q_v = [&g, qb](float v) { return q_of(g, v) == qb; };
     auto in_q_c = [ckk](uint64_t ck) { return ck >= ckk; };
@@ -2076,7 +2102,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   // usual case below, the top-p cut and the draw share one pass over the row.
   if (tid == 0) sh.dbls[1] = draw_u(a, row, P);
   __syncthreads();
-  const double u = sh.dbls[1];
+  const double u = sgpr_f64(sh.dbls[1]);
   const bool topp = P.top_p > 0.0f && P.top_p < 1.0f;
   const double tp = static_cast<double>(P.top_p);
   const double near_tp = near_topp(k);
@@ -2105,7 +2131,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     // the main pass's list holds the prefix when every element it counted was collected there (not
     // so for a capped row whose overflow bucket a tiny min-p threshold keeps); otherwise a pass
     // collects every element above a float floor just below the min-p threshold
-    int m = sh.ints[4];
+    int m = sgpr_i32(sh.ints[4]);
     __syncthreads();
     if (m != static_cast<int>(cntm)) {
       const float vlo = g.mx + static_cast<float>(static_cast<double>(P.temp) * log(thr) * 1.001) - 1e-3f;
@@ -2120,14 +2146,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         if (p < kGenCap) sh.list[p] = ck;
       });
       __syncthreads();
-      m = sh.ints[4];
+      m = sgpr_i32(sh.ints[4]);
       __syncthreads();
     }
     if (m == static_cast<int>(cntm)) {  // every kept element collected (else: the passes below)
       sort_desc(sh, sh.list, reinterpret_cast<uint64_t*>(sh.lpr), m);
       const Sel s = scan_sorted<true>(g, sh, sh.list, sh.lpr, m, 0, 0.0, topp ? tp * sum : INFINITY);
-      tot = sh.lpr[m - 1];
-      last = sh.list[m - 1];
+      tot = sgpr_f64(sh.lpr[m - 1]);
+      last = sgpr_u64(sh.list[m - 1]);
       last_from = 2;
       if (topp) apply_topp(s);
       target = u * tot;
@@ -2140,15 +2166,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const double tgt = tp * sum;
     const int qp = find_bucket(tgt);
     if (qp < kGenBuckets) {
-      const int ra_p = qp > 0 ? static_cast<int>(sh.cnt0[qp - 1]) : 0;
-      const int n_p = static_cast<int>(sh.cnt0[qp]) - ra_p;
-      const double above_p = qp > 0 ? sh.mass0[qp - 1] : 0.0;
+      const int ra_p = qp > 0 ? sgpr_i32(static_cast<int>(sh.cnt0[qp - 1])) : 0;
+      const int cnt_p = sgpr_i32(static_cast<int>(sh.cnt0[qp]));
+      const int n_p = cnt_p - ra_p;
+      const double above_p = qp > 0 ? sgpr_f64(sh.mass0[qp - 1]) : 0.0;
       // (qp = 0, the cut inside the maximum's bucket, gives d_lo = 0: bucket 0 holds the maximum)
-      if (static_cast<int>(sh.cnt0[qp]) < keep && n_p <= kGenCap / 2) {
+      if (cnt_p < keep && n_p <= kGenCap / 2) {
         const int d_lo = find_bucket(u * above_p);
-        const int d_hi = find_bucket(u * sh.mass0[qp] * (1.0 + 1e-12));  // slack: tot's sum order differs
-        const int base_d = d_lo > 0 ? static_cast<int>(sh.cnt0[d_lo - 1]) : 0;
-        if (d_hi < kGenBuckets && static_cast<int>(sh.cnt0[d_hi]) - base_d <= kGenCap / 2) {
+        const int d_hi = find_bucket(u * sgpr_f64(sh.mass0[qp]) * (1.0 + 1e-12));  // slack: tot's sum order differs
+        const int base_d = d_lo > 0 ? sgpr_i32(static_cast<int>(sh.cnt0[d_lo - 1])) : 0;
+        if (d_hi < kGenBuckets && sgpr_i32(static_cast<int>(sh.cnt0[d_hi])) - base_d <= kGenCap / 2) {
           shared = true;
           uint64_t* listA = sh.list;
           uint64_t* listB = sh.list + kGenCap / 2;
@@ -2176,16 +2203,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
             }
           });
           __syncthreads();
-          const int mA = min(sh.ints[4], kGenCap / 2), mB = min(sh.ints[7], kGenCap / 2);
+          const int mA = min(sgpr_i32(sh.ints[4]), kGenCap / 2), mB = min(sgpr_i32(sh.ints[7]), kGenCap / 2);
           sort_desc(sh, listA, reinterpret_cast<uint64_t*>(lprA), mA);
           apply_topp(scan_sorted<true>(g, sh, listA, lprA, mA, ra_p, above_p, tgt));
           target = u * tot;
           const int qd = find_bucket(target);
           if (qd >= d_lo && qd <= d_hi) {
             sort_desc(sh, listB, reinterpret_cast<uint64_t*>(lprB), mB);
-            const int ra_d = qd > 0 ? static_cast<int>(sh.cnt0[qd - 1]) : 0;
-            const int n_d = static_cast<int>(sh.cnt0[qd]) - ra_d;
-            const double above_d = qd > 0 ? sh.mass0[qd - 1] : 0.0;
+            const int ra_d = qd > 0 ? sgpr_i32(static_cast<int>(sh.cnt0[qd - 1])) : 0;
+            const int n_d = sgpr_i32(static_cast<int>(sh.cnt0[qd])) - ra_d;
+            const double above_d = qd > 0 ? sgpr_f64(sh.mass0[qd - 1]) : 0.0;
             d = scan_sorted<true>(g, sh, listB + (ra_d - base_d), lprB + (ra_d - base_d), n_d, ra_d, above_d, target);
             drawn = true;
             flags |= VSMP_FLAG_ONE_PASS;
