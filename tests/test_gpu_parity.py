@@ -141,6 +141,41 @@ def test_edge_rows(ctx, mode):
             Run(ctx, lg, p, h, off, u=np.full(len(rows), u), cand_cap=64).report()
 
 
+def test_maximum_first_index(ctx, mode):
+    """The general path's row maximum and its first index (src/sampler.cpp:72-78: value descending,
+    then index ascending; -0 == +0), where one thread meets the maximum in several of its 16-byte
+    groups (at 512 and 1024 threads a thread's groups lie 2,048 and 4,096 elements apart), in a lone
+    element past the last whole group, and among -inf. u = 0 draws the first element of the order."""
+    Vv = 20001
+    rng = np.random.default_rng(77)
+    base = -1.0 - rng.random(Vv).astype(np.float32)
+    rows = []
+    r = base.copy(); r[4] = -0.0; r[2052] = 0.0; r[4100] = 0.0
+    rows.append(r)                                  # -0 first, +0 later in the same thread's groups
+    r = base.copy(); r[6] = 0.0; r[2054] = -0.0; r[4102] = -0.0; r[3] = -0.0
+    rows.append(r)                                  # -0 ahead of +0 in another thread's group
+    r = base.copy(); r[Vv - 1] = 2.0; r[Vv - 2] = 2.0
+    rows.append(r)                                  # the maximum twice in the ragged tail
+    r = base.copy(); r[Vv - 1] = 2.0; r[9] = 2.0; r[2057] = 2.0
+    rows.append(r)                                  # ... and earlier in whole groups
+    r = np.full(Vv, -np.inf, np.float32); r[[4097, 5, 2053]] = [0.0, -0.0, 0.0]
+    rows.append(r)                                  # -inf around signed zeros
+    r = base.copy(); r[::3] = 1.5
+    rows.append(r)                                  # the maximum in every thread's first group
+    lg = np.stack(rows)
+    for temp, top_k, top_p, min_p in [(1.0, 0, 0.9, 0.0), (0.5, 600, 0.95, 0.05), (1.0, 0, 0.5, 0.5)]:
+        p = V.params_array(n=1, temp=temp, top_k=top_k, top_p=top_p, min_p=min_p, repeat=1.0, repeat_last=0,
+                           seed=11)
+        log("maximum first index", mode, temp, top_k, top_p, min_p)
+        for u in (0.0, 0.5):
+            Run(ctx, lg, p, None, None, u=np.full(len(rows), u), cand_cap=8).report()
+    # the same rows penalised: a penalised maximum gives way to the next value
+    hists = [[4, 2052, 6, Vv - 1, 9, 5, 0]] * len(rows)
+    p = V.params_array(n=1, temp=1.0, top_k=0, top_p=0.9, min_p=0.0, repeat=1.3, repeat_last=0, seed=11)
+    log("maximum first index, penalised", mode)
+    Run(ctx, lg, p, *csr(hists), u=np.zeros(len(rows)), cand_cap=8).report()
+
+
 def test_no_history_and_padded_rows(ctx, mode):
     rng = np.random.default_rng(9)
     lg = rng.normal(0, 2, (7, 1001)).astype(np.float32)

@@ -1310,6 +1310,15 @@ __device__ __forceinline__ void gen_pass_groups(const GenRow& R, F&& f, F4&& f4)
   else
     gen_pass_loop<NT, U>(R, f, f4, [&R](int i) { return R.bits[i]; });
 }
+// Element i of the row, penalty applied, as the passes see it.
+__device__ __forceinline__ float gen_value(const GenRow& R, int i) {
+  float v = R.rp[i];
+  if (R.pen) {
+    const uint32_t w = R.lds_bits ? gen_lds_bits()[i >> 5] : R.bits[i >> 5];
+    if ((w >> (i & 31)) & 1u) v = penalise(v, R.rep);
+  }
+  return v;
+}
 template <int NT, int U = 1, class F>
 __device__ __forceinline__ void gen_pass(const GenRow& R, F&& f) {
   gen_pass_groups<NT, U>(R, f, [&f](int e, const float (&x)[4]) {
@@ -1782,13 +1791,41 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       g.R.lds_bits = true;
       if (a.pen_bits) store_pen_words<kGenThreads>(a, row, 0, lb, a.words);
     }
-    uint32_t mn = 0xFFFFFFFFu;
-    gen_pass<NT>(g.R, [&](int e, float v) {
-      const uint32_t kv = ord_key(v);
-      mxc = max64(mxc, comp(kv, static_cast<uint32_t>(e)));
-      mn = min(mn, kv);
-    });
-    mnk = mn;
+    // The largest and smallest values as floats, a 16-byte group at a time: the order keys order
+    // values as float comparison does (-0 with +0), so no key is formed per element. A lane keeps
+    // the first element of the unit (group, or lone element past the last whole group) where its
+    // running maximum last rose; the row maximum's first index lies in such a unit (the lane that
+    // holds it saw only smaller values before it), found after the reduction.
+    float rmx = -INFINITY, rmn = INFINITY;
+    int unit = -1;
+    gen_pass_groups<NT, 1>(
+        g.R,
+        [&](int e, float v) {
+          if (v > rmx) unit = e;
+          rmx = fmaxf(rmx, v);
+          rmn = fminf(rmn, v);
+        },
+        [&](int e, const float (&x)[4]) {
+          const float gm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+          if (gm > rmx) unit = e;
+          rmx = fmaxf(rmx, gm);
+          rmn = fminf(rmn, fminf(fminf(x[0], x[1]), fminf(x[2], x[3])));
+        });
+    const uint32_t kmax = static_cast<uint32_t>(block_max64<kGenThreads>(ord_key(rmx), sh.r64));
+    mnk = block_min64<kGenThreads>(ord_key(rmn), sh.r64);
+    uint32_t first = 0xFFFFFFFFu;
+    if (unit >= 0 && ord_key(rmx) == kmax) {
+      for (int c = 0; c < 4; ++c) {
+        const int i = unit + c;
+        if (i < V && ord_key(gen_value(g.R, i)) == kmax) {
+          first = static_cast<uint32_t>(i);
+          break;
+        }
+      }
+    }
+    first = static_cast<uint32_t>(block_min64<kGenThreads>(first, sh.r64));
+    // no unit rose above -inf: every element is -inf, the first is element 0
+    mxc = comp(kmax, first == 0xFFFFFFFFu ? 0u : first);
   } else {
     // row maximum / minimum from the slices (or k_rows's pass), the bitmap from scratch
     for (int i = tid; i < S; i += kGenThreads) {
@@ -1801,9 +1838,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       __syncthreads();
       g.R.lds_bits = true;
     }
+    mxc = block_max64<kGenThreads>(mxc, sh.r64);
+    mnk = block_min64<kGenThreads>(mnk, sh.r64);
   }
-  mxc = block_max64<kGenThreads>(mxc, sh.r64);
-  mnk = block_min64<kGenThreads>(mnk, sh.r64);
   g.mx = comp_val(mxc);
   g.temp = P.temp;
   g.inv_temp = 1.0 / static_cast<double>(P.temp);
