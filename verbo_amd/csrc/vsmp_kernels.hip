@@ -1349,6 +1349,7 @@ struct __align__(16) GenShared {  // list is read as 16-byte vectors
   double rd[kGenNW];
   uint32_t r32[kGenNW];
   int ints[8];
+  int fb[4];  // the bucket searches' results
   uint64_t u64s[4];
   double dbls[4];
 };
@@ -2024,10 +2025,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     });
     return block_min64<kGenThreads>(t, sh.r64);
   };
-  // level-0 inclusive prefixes (4 buckets per thread, bucket 0 = closest to the maximum)
+  // level-0 inclusive prefixes (BP consecutive buckets per thread, bucket 0 = closest to the maximum)
+  constexpr int BP = kGenBuckets / kGenThreads;
+  static_assert(BP % 4 == 0, "a thread's buckets are read as 16-byte vectors");
+  const int b0 = BP * tid;
   {
-    constexpr int BP = kGenBuckets / kGenThreads;  // consecutive buckets per thread
-    const int b0 = BP * tid;
     double m[BP];
     uint32_t c[BP];
     double ms = 0.0;
@@ -2051,6 +2053,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       sh.mass0[b0 + i] = em;
       sh.cnt0[b0 + i] = ec;
     }
+    if (tid < 4) sh.fb[tid] = kGenBuckets;
     __syncthreads();
   }
   // the sum over the top-k prefix (src/sampler.cpp:84): the histogram's total
@@ -2075,17 +2078,42 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   }
   const int keep_minp = keep;
 
-  // The first non-empty level-0 bucket whose inclusive mass reaches target (kGenBuckets: none).
+  // The first non-empty level-0 bucket whose inclusive mass reaches target (kGenBuckets: none), each
+  // thread looking in its own BP consecutive buckets (read as 16-byte vectors). The k-th search
+  // takes its minimum in slot k % 4 and clears slot (k + 2) % 4 for a later search: every thread
+  // read that slot's last result before the previous search's barrier, and the next barrier orders
+  // the clearing before its reuse. One barrier per search.
+  int fb_call = 0;
   auto find_bucket = [&](double target) -> int {
-    if (tid == 0) sh.ints[6] = kGenBuckets;
-    __syncthreads();
-    for (int b = tid; b < kGenBuckets; b += kGenThreads) {
-      const uint32_t prev = b > 0 ? sh.cnt0[b - 1] : 0u;
-      wave_claim_min(&sh.ints[6], sh.cnt0[b] > prev && sh.mass0[b] >= target, b);
+    double pm[BP];
+    uint32_t pc[BP];
+#pragma unroll
+    for (int i = 0; i < BP; i += 2) {
+      const double2 t = *reinterpret_cast<const double2*>(&sh.mass0[b0 + i]);
+      pm[i] = t.x;
+      pm[i + 1] = t.y;
     }
+#pragma unroll
+    for (int i = 0; i < BP; i += 4) {
+      const uint4 t = *reinterpret_cast<const uint4*>(&sh.cnt0[b0 + i]);
+      pc[i] = t.x;
+      pc[i + 1] = t.y;
+      pc[i + 2] = t.z;
+      pc[i + 3] = t.w;
+    }
+    int first = kGenBuckets;
+    uint32_t prev = b0 > 0 ? sh.cnt0[b0 - 1] : 0u;
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
+      if (first == kGenBuckets && pc[i] > prev && pm[i] >= target) first = b0 + i;
+      prev = pc[i];
+    }
+    int* slot = &sh.fb[fb_call & 3];
+    wave_claim_min(slot, first < kGenBuckets, first);  // a thread's buckets rise with its lane
+    if (tid == 0) sh.fb[(fb_call + 2) & 3] = kGenBuckets;
     __syncthreads();
-    const int qb = sgpr_i32(sh.ints[6]);
-    __syncthreads();
+    const int qb = sgpr_i32(*slot);
+    ++fb_call;
     return qb;
   };
   auto first_element = [&]() -> Sel {  // the first element already reaches the target (src/sampler.cpp:105-106)
