@@ -1251,7 +1251,7 @@ __device__ __forceinline__ uint32_t* gen_lds_bits() {
 // loads in flight (a and b); every load is issued unconditionally (past the row it rereads the last
 // 16-byte group, which 4*ceil(V/4) <= ld keeps inside the row), so each wait covers exactly the
 // buffer about to be processed.
-template <int NT, int U, class F, class F4, class W>
+template <int NT, int U, bool Rev, class F, class F4, class W>
 __device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, F4&& f4, W&& word) {
   constexpr int kGenThreads = NT;
   constexpr int step = kGenThreads * 4 * U;
@@ -1259,15 +1259,19 @@ __device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, F4&& f4, W
   const float4* rp4 = reinterpret_cast<const float4*>(R.rp);
   const int V4 = (R.V + 3) >> 2;
   const int nit = (R.V + step - 1) / step;
+  // Rev: the row's blocks last to first (block it of the loop is block nit - 1 - it), so that a pass
+  // following another starts on the lines that pass read last
+  auto blk = [&](int it) { return Rev ? nit - 1 - it : it; };
   float4 a[U], b[U];
   auto load = [&](int it, float4 (&v)[U]) {
+    const int bi = max(blk(it), 0);  // past the loop's end (Rev): the first block again
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = rp4[min(it * (step / 4) + u * kGenThreads + tid, V4 - 1)];
+    for (int u = 0; u < U; ++u) v[u] = rp4[min(bi * (step / 4) + u * kGenThreads + tid, V4 - 1)];
   };
   auto process = [&](int it, const float4 (&v)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int e = it * step + (u * kGenThreads + tid) * 4;
+      const int e = blk(it) * step + (u * kGenThreads + tid) * 4;
       if (e >= R.V) continue;
       float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
       if (R.pen) {
@@ -1303,12 +1307,12 @@ __device__ __forceinline__ void gen_pass_loop(const GenRow& R, F&& f, F4&& f4, W
 // 16-byte group, which lets a caller order the work of four elements itself. U: 16-byte loads per
 // thread and buffer (two buffers in flight); U = 4 for the select passes measured slower (the
 // kernel's code grows by half and every phase slows), so every pass takes U = 1.
-template <int NT, int U, class F, class F4>
+template <int NT, int U, bool Rev = false, class F, class F4>
 __device__ __forceinline__ void gen_pass_groups(const GenRow& R, F&& f, F4&& f4) {
   if (R.lds_bits)
-    gen_pass_loop<NT, U>(R, f, f4, [](int i) { return gen_lds_bits()[i]; });
+    gen_pass_loop<NT, U, Rev>(R, f, f4, [](int i) { return gen_lds_bits()[i]; });
   else
-    gen_pass_loop<NT, U>(R, f, f4, [&R](int i) { return R.bits[i]; });
+    gen_pass_loop<NT, U, Rev>(R, f, f4, [&R](int i) { return R.bits[i]; });
 }
 // Element i of the row, penalty applied, as the passes see it.
 __device__ __forceinline__ float gen_value(const GenRow& R, int i) {
@@ -1938,7 +1942,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         }
       }
     };
-    gen_pass_groups<NT, 1>(
+    gen_pass_groups<NT, 1, true>(  // after the maximum pass: its last lines first
         g.R,
         [&](int e, float v) {
           const float d = v - g.mx;
