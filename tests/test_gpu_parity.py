@@ -176,6 +176,29 @@ def test_maximum_first_index(ctx, mode):
     Run(ctx, lg, p, *csr(hists), u=np.zeros(len(rows)), cand_cap=8).report()
 
 
+def test_general_full_buckets(ctx, mode):
+    """The general path on rows where one level-0 bucket holds thousands of elements (its histogram
+    adds all meet on one address): one value repeated 7,990, 8,100, 9,000 and 70,000 times among
+    N(0, 1) values, with top-p, a capped row (temp .02), a top-k cut and min-p."""
+    rng = np.random.default_rng(515)
+    rows = []
+    for Vv, n_eq in ((30000, 7990), (30000, 8100), (30000, 9000), (151936, 70000)):
+        r = rng.normal(0, 1, Vv).astype(np.float32)
+        pos = rng.choice(Vv, n_eq, replace=False)
+        r[pos] = np.float32(0.25)
+        rows.append(r)
+    for r in rows:
+        Vv = r.size
+        lg = r[None, :]
+        for temp, top_k, top_p, min_p in [(1.0, 0, 0.9, 0.0), (0.02, 0, 0.95, 0.0), (0.8, 1000, 0.9, 0.0),
+                                          (1.0, 0, 0.99, 0.01)]:
+            p = V.params_array(n=1, temp=temp, top_k=top_k, top_p=top_p, min_p=min_p, repeat=1.0, repeat_last=0,
+                               seed=5)
+            log("full buckets", mode, Vv, temp, top_k, top_p, min_p)
+            for u in (0.3, 0.999):
+                Run(ctx, lg, p, None, None, u=np.full(1, u), cand_cap=16).report()
+
+
 def test_no_history_and_padded_rows(ctx, mode):
     rng = np.random.default_rng(9)
     lg = rng.normal(0, 2, (7, 1001)).astype(np.float32)
