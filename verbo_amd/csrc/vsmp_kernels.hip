@@ -1469,21 +1469,40 @@ __device__ __forceinline__ double numer_tab(const GenCtx& g, const double* etab,
   return fma(e * r, s, e);
 }
 
-// The main pass's mass of an element of bucket q relative to its table point: exp(x - c_(q >> 1))
-// (within e^(+-1/64) of 1) as a fixed-point integer of 2^-40 units, rounded to nearest by one fma
-// (4097 + r s has a 2^-40 ulp; its low 52 bits are the value's). Bucket q's mass is then
+// The main pass's mass of an element of bucket q relative to its table point: exp(r), r = x -
+// c_(q >> 1) (within e^(+-1/64) of 1), as a fixed-point integer of 2^-40 units, rounded to nearest
+// by one fma: t = 4097 + (exp(r) - 1) has a 2^-40 ulp in [4096, 8192), so t's bits are kFixRawE
+// (its exponent field) plus the value. The bits are what the pass adds: a bucket of n elements
+// holds n kFixRawE + its sum (mod 2^64), taken apart in the prefix. Bucket q's mass is then
 // etab[q >> 1] * sum * 2^-40: the sums exact and order-free (at most 2^20 terms of under 2^40.03
 // each), each term within 5e-13 (relative) of exp(x): 2^-41 e^(1/64) = 4.6e-13 of rounding, and
 // 2.1e-14 for the degree-5 Taylor polynomial of exp(r), |r| <= 1/64, that the rounding allows.
-__device__ __forceinline__ uint64_t numer_fix(const GenCtx& g, double w, float d, int q) {
-  const double x = static_cast<double>(d) * g.inv_temp;
-  const double r = fma(static_cast<double>(q | 1), w, x);
-  double s = fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);  // 1/120, 1/24
-  s = fma(r, s, 0x1.5555555555555p-3);                             // 1/6
-  s = fma(r, s, 0.5);
-  s = fma(r, s, 1.0);
-  const double t = fma(r, s, 4097.0);
-  return static_cast<uint64_t>(__double_as_longlong(t)) & ((1ull << 52) - 1ull);
+// The polynomial is taken in z = d + (2j + 1) w temp = r temp, its coefficients a_k = 1 / (k!
+// temp^k), so that r is never formed: z's two roundings put r within 64 2^-52 temp of its value,
+// 2^-46 at most.
+struct FixCoef {
+  double wt;                  // w temp
+  double a1, a2, a3, a4, a5;  // (1 / temp)^k / k!
+};
+__device__ __forceinline__ FixCoef fix_coef(double w, float temp, double inv_temp) {
+  FixCoef c;
+  c.wt = w * static_cast<double>(temp);
+  c.a1 = inv_temp;
+  c.a2 = c.a1 * inv_temp * 0.5;
+  c.a3 = c.a2 * inv_temp * (1.0 / 3.0);
+  c.a4 = c.a3 * inv_temp * 0.25;
+  c.a5 = c.a4 * inv_temp * 0.2;
+  return c;
+}
+constexpr uint64_t kFixRawE = 0x40B0000000000000ull;  // the bits of 4096.0
+__device__ __forceinline__ uint64_t numer_fix(const FixCoef& c, float d, int q) {
+  const double z = fma(static_cast<double>(q | 1), c.wt, static_cast<double>(d));
+  double s = fma(z, c.a5, c.a4);
+  s = fma(z, s, c.a3);
+  s = fma(z, s, c.a2);
+  s = fma(z, s, c.a1);
+  const double t = fma(z, s, 4097.0);
+  return static_cast<uint64_t>(__double_as_longlong(t));
 }
 constexpr double kFixUnit = 0x1p-40;
 
@@ -1890,6 +1909,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   double* etab = sh.rmass;
   const double wq = table_width(g.qs, P.temp);
   for (int j = tid; j < kGenBuckets / 2; j += kGenThreads) etab[j] = exp_tab(-static_cast<double>(2 * j + 1) * wq);
+  const FixCoef fc = fix_coef(wq, P.temp, g.inv_temp);
   // The main pass also collects the min-p prefix (its elements' exact numerators are taken there)
   // into the list, which aliases the refinement counts, idle until the pass ends.
   if (tid == 0) sh.ints[4] = 0;
@@ -1947,7 +1967,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         [&](int e, float v) {
           const float d = v - g.mx;
           const int q = q_of_d(g, d);
-          if (!excluded(e, v)) add(e, v, d, q, numer_fix(g, wq, d, q));
+          if (!excluded(e, v)) add(e, v, d, q, numer_fix(fc, d, q));
         },
         // the four masses first, then the four elements' histogram atomics together
         [&](int e, const float (&x)[4]) {
@@ -1958,7 +1978,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
           for (int c = 0; c < 4; ++c) {
             d[c] = x[c] - g.mx;
             q[c] = q_of_d(g, d[c]);
-            f[c] = numer_fix(g, wq, d[c], q[c]);
+            f[c] = numer_fix(fc, d[c], q[c]);
           }
 #pragma unroll
           for (int c = 0; c < 4; ++c)
@@ -1978,7 +1998,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const int n_in = cut_k ? k : V;
     if (tid == 0) {
       sh.cnt0[0] = static_cast<uint32_t>(n_in);
-      fix0[0] = static_cast<uint64_t>(n_in) << 40;
+      fix0[0] = static_cast<uint64_t>(n_in) * (kFixRawE + (1ull << 40));  // n_in bits of 4097.0
     }
     if (minp && 1.0 >= thr) {
       if (tid == 0) {
@@ -2041,9 +2061,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
 #pragma unroll
     for (int i = 0; i < BP; ++i) {
       const int b = b0 + i;
-      m[i] = etab[b >> 1] * (static_cast<double>(fix0[b]) * kFixUnit);
-      if (b == kGenBuckets - 1) m[i] += sh.dbls[2];
       c[i] = sh.cnt0[b];
+      // the bits added are kFixRawE plus the value per element; a capped row's last bucket took none
+      const uint64_t nraw = (capped && b == kGenBuckets - 1) ? 0ull : c[i];
+      m[i] = etab[b >> 1] * (static_cast<double>(fix0[b] - nraw * kFixRawE) * kFixUnit);
+      if (b == kGenBuckets - 1) m[i] += sh.dbls[2];
       ms += m[i];
       cs += c[i];
     }
@@ -3887,11 +3909,12 @@ __global__ __launch_bounds__(256) void k_numer_probe(const float* __restrict__ d
   g.qs = qs;
   const double wq = table_width(qs, temp);
   for (int j = threadIdx.x; j < kGenBuckets / 2; j += 256) etab[j] = exp_tab(-static_cast<double>(2 * j + 1) * wq);
+  const FixCoef fc = fix_coef(wq, temp, g.inv_temp);
   __syncthreads();
   const long long stride = static_cast<long long>(gridDim.x) * 256;
   for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
     const int q = max(q_of_d(g, d[i]), 0);  // d > 0 (no row holds one) kept in range
-    y[i] = fixed_point ? etab[q >> 1] * (static_cast<double>(numer_fix(g, wq, d[i], q)) * kFixUnit)
+    y[i] = fixed_point ? etab[q >> 1] * (static_cast<double>(numer_fix(fc, d[i], q) - kFixRawE) * kFixUnit)
                        : numer_tab(g, etab, wq, d[i], q);
   }
 }
