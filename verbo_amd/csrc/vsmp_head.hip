@@ -76,6 +76,41 @@ __device__ __forceinline__ void mma_chunk(const uint16_t* X, const uint16_t* W, 
   }
 }
 
+// mma_chunk with the next chunk's LDS stores spread over its steps: after the MFMAs of step s, the
+// stores of pieces q with q % 4 == s (x and w), so that the fragment reads of the first steps do not
+// queue behind all of them.
+template <int WMB, int WNB, int QX, int QW, int NT, int NPX, int NPW>
+__device__ __forceinline__ void mma_chunk_st(const uint16_t* X, const uint16_t* W, int ra, int cb, int ko,
+                                             f32x16 (&acc)[WMB][WNB], uint16_t* nX, uint16_t* nW,
+                                             const u32x4 (&px)[QX], const u32x4 (&pw)[QW]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int s = 0; s < kHeadKC / 16; ++s) {
+    bf16x8 a[WMB], b[WNB];
+#pragma unroll
+    for (int i = 0; i < WMB; ++i) a[i] = *reinterpret_cast<const bf16x8*>(&X[(ra + 32 * i) * kHStr + ko + 8 * s]);
+#pragma unroll
+    for (int j = 0; j < WNB; ++j) b[j] = *reinterpret_cast<const bf16x8*>(&W[(cb + 32 * j) * kHStr + ko + 8 * s]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < WMB; ++i)
+#pragma unroll
+      for (int j = 0; j < WNB; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = s; q < QX; q += 4) {
+      const int p = tid + q * NT;
+      if (NPX % NT == 0 || p < NPX) *reinterpret_cast<u32x4*>(&nX[(p >> 3) * kHStr + 8 * (p & 7)]) = px[q];
+    }
+#pragma unroll
+    for (int q = s; q < QW; q += 4) {
+      const int p = tid + q * NT;
+      if (NPW % NT == 0 || p < NPW) *reinterpret_cast<u32x4*>(&nW[(p >> 3) * kHStr + 8 * (p & 7)]) = pw[q];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // WMB x WNB blocks of 32 x 32 per wave, WM x WN waves, R chunks in flight per thread (a ring of
 // registers: chunk c is loaded R chunks before it is used, and loads are consumed in the order they
 // were issued, so each wait covers only the oldest chunk), two LDS stages.
@@ -149,9 +184,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_head_gemm(HeadArgs h) {
       const int c = c0 + r;
       __syncthreads();  // stage c % 2 holds chunk c; stage (c + 1) % 2 is no longer read
       const int rn = (r + 1) % R;
-      chunk_store<QX, QW, NT, NPX, NPW>(sX[(r + 1) & 1], sW[(r + 1) & 1], rx[rn], rw[rn]);
+      mma_chunk_st<WMB, WNB, QX, QW, NT, NPX, NPW>(sX[r & 1], sW[r & 1], ra, cb, ko, acc, sX[(r + 1) & 1], sW[(r + 1) & 1],
+                                                   rx[rn], rw[rn]);
       chunk_load<QX, QW, NT, NPX, NPW>(xb, wb, xo, wo, min(c + 1 + R, nch - 1) * kHeadKC, rx[rn], rw[rn]);
-      mma_chunk<WMB, WNB>(sX[r & 1], sW[r & 1], ra, cb, ko, acc);
     }
   }
 #pragma unroll
